@@ -1,0 +1,50 @@
+// Internal interface between the flash C-ABI entry points and the per-dtype kernels.
+#pragma once
+
+#include "pnfx_common.h"
+
+namespace pnfx {
+
+struct FwdParams {
+  const void *q, *k, *v;
+  void* o;
+  int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
+  float* M;
+  float* Z;
+  int32_t* Nmax;
+  uint8_t* mask;
+  int B, H, N, nq32, nk64;
+  const float* tau;
+  float scale, gamma;
+};
+
+struct BwdParams {
+  const void *q, *k, *v, *o, *dout;
+  void *dq, *dk, *dv;
+  int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn, dosb, dosh, dosn;
+  int64_t dqsb, dqsh, dqsn, dksb, dksh, dksn, dvsb, dvsh, dvsn;
+  const float* M;
+  const float* Z;
+  const int32_t* Nmax;
+  const uint8_t* mask;
+  float* rc;        // row constants [B*H*N][8]: M, r = g/Z, c = 10 g/Z * scale, Dv, G
+  float* partials;  // tau partials [B*H][nkvb][4]
+  float* dtau;
+  int B, H, N, nq32, nk64, nkvb;
+  const float* tau;
+  float scale, gamma;
+};
+
+// Key blocks of the key-parallel backward kernel (also sizes the tau partials).
+inline int bwd_nkvb(int64_t N, int64_t D) {
+  const int64_t bnk = D <= 64 ? 128 : 64;
+  return (int)((N + bnk - 1) / bnk);
+}
+int64_t bwd_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D);
+
+int flash_fwd_bf16(const FwdParams& fp, int64_t D, bool causal, bool has_gamma, hipStream_t st);
+int flash_bwd_bf16(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, hipStream_t st);
+int flash_fwd_f32(const FwdParams& fp, int64_t D, bool causal, bool has_gamma, hipStream_t st);
+int flash_bwd_f32(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, hipStream_t st);
+
+}  // namespace pnfx

@@ -1,0 +1,103 @@
+// C-ABI entry points of the flash path: argument checks, workspace carving, dtype dispatch.
+#include "flash.h"
+
+namespace pnfx {
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Each [B, H, N, D] operand must have unit inner stride; the bf16 MFMA kernels read and
+// write whole 16-byte (8-element) chunks of a row.
+int check_operand(const char* name, const void* p, int64_t sb, int64_t sh, int64_t sn, int dtype) {
+  PNFX_REQUIRE(p != nullptr, "flash: %s is null", name);
+  if (dtype == PNFX_BF16) {
+    PNFX_REQUIRE(aligned16(p) && sb % 8 == 0 && sh % 8 == 0 && sn % 8 == 0,
+                 "flash: %s must be 16-byte aligned with strides that are multiples of 8 "
+                 "elements (got %lld, %lld, %lld)",
+                 name, (long long)sb, (long long)sh, (long long)sn);
+  }
+  return PNFX_OK;
+}
+
+int check_shape(int64_t B, int64_t H, int64_t N, int64_t D) {
+  PNFX_REQUIRE(B >= 1 && H >= 1 && N >= 1, "flash: bad shape B=%lld H=%lld N=%lld", (long long)B,
+               (long long)H, (long long)N);
+  PNFX_REQUIRE(D == 16 || D == 32 || D == 64 || D == 128, "flash: head dim %lld not in {16,32,64,128}",
+               (long long)D);
+  PNFX_REQUIRE(B * H <= (1ll << 30) && N <= (1ll << 28) && B * H * ((N + 127) / 128) < (1ll << 31),
+               "flash: shape too large for the launch grid");
+  return PNFX_OK;
+}
+
+}  // namespace
+}  // namespace pnfx
+
+using namespace pnfx;
+
+extern "C" int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
+                              int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
+                              int64_t vsh, int64_t vsn, void* o, int64_t osb, int64_t osh,
+                              int64_t osn, float* M, float* Z, int32_t* Nmax, uint8_t* tile_mask,
+                              int64_t B, int64_t H, int64_t N, int64_t D, const float* tau,
+                              float scale, float gamma, int has_gamma, int causal, int dtype,
+                              void* stream) {
+  int rc;
+  if ((rc = check_shape(B, H, N, D))) return rc;
+  PNFX_REQUIRE(dtype == PNFX_BF16 || dtype == PNFX_F32, "flash: unsupported dtype %d", dtype);
+  if ((rc = check_operand("q", q, qsb, qsh, qsn, dtype))) return rc;
+  if ((rc = check_operand("k", k, ksb, ksh, ksn, dtype))) return rc;
+  if ((rc = check_operand("v", v, vsb, vsh, vsn, dtype))) return rc;
+  if ((rc = check_operand("o", o, osb, osh, osn, dtype))) return rc;
+  PNFX_REQUIRE(M && Z && Nmax && tau, "flash_fwd: null statistics / tau pointer");
+  FwdParams fp{q, k, v, o, qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn,
+               M, Z, Nmax, tile_mask, (int)B, (int)H, (int)N,
+               (int)((N + 31) / 32), (int)((N + 63) / 64), tau, scale, gamma};
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  return dtype == PNFX_BF16 ? flash_fwd_bf16(fp, D, causal != 0, has_gamma != 0, st)
+                            : flash_fwd_f32(fp, D, causal != 0, has_gamma != 0, st);
+}
+
+extern "C" int64_t pnfx_flash_bwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D) {
+  return bwd_workspace_bytes(B, H, N, D);
+}
+
+extern "C" int pnfx_flash_bwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
+                              int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
+                              int64_t vsh, int64_t vsn, const void* o, int64_t osb, int64_t osh,
+                              int64_t osn, const void* dout, int64_t dosb, int64_t dosh,
+                              int64_t dosn, const float* M, const float* Z, const int32_t* Nmax,
+                              const uint8_t* tile_mask, void* dq, int64_t dqsb, int64_t dqsh,
+                              int64_t dqsn, void* dk, int64_t dksb, int64_t dksh, int64_t dksn,
+                              void* dv, int64_t dvsb, int64_t dvsh, int64_t dvsn, float* dtau,
+                              void* workspace, int64_t workspace_bytes, int64_t B, int64_t H,
+                              int64_t N, int64_t D, const float* tau, float scale, float gamma,
+                              int has_gamma, int causal, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_shape(B, H, N, D))) return rc;
+  PNFX_REQUIRE(dtype == PNFX_BF16 || dtype == PNFX_F32, "flash: unsupported dtype %d", dtype);
+  if ((rc = check_operand("q", q, qsb, qsh, qsn, dtype))) return rc;
+  if ((rc = check_operand("k", k, ksb, ksh, ksn, dtype))) return rc;
+  if ((rc = check_operand("v", v, vsb, vsh, vsn, dtype))) return rc;
+  if ((rc = check_operand("o", o, osb, osh, osn, dtype))) return rc;
+  if ((rc = check_operand("dout", dout, dosb, dosh, dosn, dtype))) return rc;
+  if ((rc = check_operand("dq", dq, dqsb, dqsh, dqsn, dtype))) return rc;
+  if ((rc = check_operand("dk", dk, dksb, dksh, dksn, dtype))) return rc;
+  if ((rc = check_operand("dv", dv, dvsb, dvsh, dvsn, dtype))) return rc;
+  PNFX_REQUIRE(M && Z && Nmax && tau && dtau, "flash_bwd: null statistics / tau pointer");
+  const int64_t need = bwd_workspace_bytes(B, H, N, D);
+  PNFX_REQUIRE(workspace && workspace_bytes >= need && (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
+               "flash_bwd: workspace needs %lld bytes, 256-byte aligned (got %lld)", (long long)need,
+               (long long)workspace_bytes);
+  const int64_t rc_bytes = ((B * H * N * 8 * 4 + 255) / 256) * 256;
+  float* rcbuf = static_cast<float*>(workspace);
+  float* parts = reinterpret_cast<float*>(static_cast<char*>(workspace) + rc_bytes);
+  BwdParams bp{q, k, v, o, dout, dq, dk, dv,
+               qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn, dosb, dosh, dosn,
+               dqsb, dqsh, dqsn, dksb, dksh, dksn, dvsb, dvsh, dvsn,
+               M, Z, Nmax, tile_mask, rcbuf, parts, dtau,
+               (int)B, (int)H, (int)N, (int)((N + 31) / 32), (int)((N + 63) / 64),
+               bwd_nkvb(N, D), tau, scale, gamma};
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  return dtype == PNFX_BF16 ? flash_bwd_bf16(bp, D, causal != 0, has_gamma != 0, st)
+                            : flash_bwd_f32(bp, D, causal != 0, has_gamma != 0, st);
+}

@@ -1,0 +1,283 @@
+"""torch.library custom ops over libpnfx.so (namespace ``pnfx``), with autograd.
+
+Each op allocates its outputs with the caching allocator on the input's device,
+enqueues the HIP kernels on the current stream through the C ABI, and never
+blocks the host.  Ops are registered for the CUDA (= HIP) device only: calling
+them on CPU tensors raises, and a missing library raises ``PnfxError``.
+
+Op                     reference counterpart (src/triton_pnfirtau.py)
+pnfx::fir_fwd / _bwd   _TritonCausalFir7Fn              :629-682
+pnfx::pn_rows_fwd/_bwd _TritonPnFirTauScoresFn          :694-785
+pnfx::flash_fwd/_bwd   _FlashPnFirTauFn                 :814-968
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_DT = {torch.float32: _lib.PNFX_F32, torch.bfloat16: _lib.PNFX_BF16}
+
+
+def _code(t: Tensor, what: str) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"{what}: dtype {t.dtype} is not supported (float32, bfloat16)") from None
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _tau32(tau: Tensor) -> Tensor:
+    t = tau.detach().reshape(1)
+    return t if t.dtype == torch.float32 else t.to(torch.float32)
+
+
+def _as_bhnc(x: Tensor) -> tuple[Tensor, int, int, int, int]:
+    """View x ([B,N,C] or [B,H,N,C]) as 4-D with unit channel stride; returns (x4, B, H, N, C)."""
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    x4 = x.unsqueeze(1) if x.dim() == 3 else x
+    if x4.dim() != 4:
+        raise ValueError(f"FIR input must be [B,N,C] or [B,H,N,C], got {tuple(x.shape)}")
+    B, H, N, C = x4.shape
+    return x4, B, H, N, C
+
+
+# ---------------------------------------------------------------------------- FIR
+def _fir_call(x: Tensor, taps: Tensor, adjoint: bool) -> Tensor:
+    x4, B, H, N, C = _as_bhnc(x)
+    taps2 = taps.reshape(-1, taps.shape[-1])
+    if taps2.dtype != torch.float32 or not taps2.is_contiguous() or taps2.device != x.device:
+        taps2 = taps2.to(device=x.device, dtype=torch.float32).contiguous()
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    fn = _lib.lib().pnfx_fir_bwd if adjoint else _lib.lib().pnfx_fir_fwd
+    rc = fn(x4.data_ptr(), x4.stride(0), x4.stride(1), x4.stride(2), y.data_ptr(), B, H, N, C,
+            taps2.data_ptr(), taps2.shape[0], taps2.shape[1], _code(x, "fir"), _stream(x))
+    _lib.check(rc, "pnfx_fir_bwd" if adjoint else "pnfx_fir_fwd")
+    return y
+
+
+@torch.library.custom_op("pnfx::fir_fwd", mutates_args=(), device_types="cuda")
+def fir_fwd(x: Tensor, taps: Tensor) -> Tensor:
+    """Causal FIR along N of x [B,N,C] or [B,H,N,C]; taps fp32 [K] or [H,K] (oldest lag first)."""
+    return _fir_call(x, taps, False)
+
+
+@torch.library.custom_op("pnfx::fir_bwd", mutates_args=(), device_types="cuda")
+def fir_bwd(gy: Tensor, taps: Tensor) -> Tensor:
+    """Adjoint of fir_fwd (anti-causal correlation with the same taps)."""
+    return _fir_call(gy, taps, True)
+
+
+@fir_fwd.register_fake
+def _(x, taps):
+    return torch.empty(x.shape, dtype=x.dtype, device=x.device)
+
+
+@fir_bwd.register_fake
+def _(gy, taps):
+    return torch.empty(gy.shape, dtype=gy.dtype, device=gy.device)
+
+
+def _fir_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[1])
+
+
+def _fir_backward(ctx, gy):
+    (taps,) = ctx.saved_tensors
+    return fir_bwd(gy, taps), None
+
+
+torch.library.register_autograd("pnfx::fir_fwd", _fir_backward, setup_context=_fir_setup)
+
+
+# ---------------------------------------------------------------------------- row scores
+@torch.library.custom_op("pnfx::pn_rows_fwd", mutates_args=(), device_types="cuda")
+def pn_rows_fwd(raw: Tensor, tau: Tensor, scale: float, p: float, gamma: float, has_gamma: bool,
+                causal: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Row-fused score -> weight over raw [..., N, N]; returns (W, M, Z, Nmax), stats per row."""
+    N = raw.shape[-1]
+    r2 = raw.contiguous().view(-1, N)
+    R = r2.shape[0]
+    w = torch.empty_like(r2)
+    M = torch.empty(R, device=raw.device, dtype=torch.float32)
+    Z = torch.empty(R, device=raw.device, dtype=torch.float32)
+    Nm = torch.empty(R, device=raw.device, dtype=torch.int32)
+    t32 = _tau32(tau)
+    rc = _lib.lib().pnfx_pn_rows_fwd(r2.data_ptr(), N, w.data_ptr(), N, M.data_ptr(), Z.data_ptr(),
+                                     Nm.data_ptr(), R, N, t32.data_ptr(), scale, p, gamma,
+                                     int(has_gamma), int(causal), _code(raw, "pn_rows"),
+                                     _stream(raw))
+    _lib.check(rc, "pnfx_pn_rows_fwd")
+    return w.view(raw.shape), M, Z, Nm
+
+
+@pn_rows_fwd.register_fake
+def _(raw, tau, scale, p, gamma, has_gamma, causal):
+    R = raw.numel() // max(raw.shape[-1], 1)
+    f = lambda dt: torch.empty(R, device=raw.device, dtype=dt)  # noqa: E731
+    return torch.empty_like(raw), f(torch.float32), f(torch.float32), f(torch.int32)
+
+
+@torch.library.custom_op("pnfx::pn_rows_bwd", mutates_args=(), device_types="cuda")
+def pn_rows_bwd(dw: Tensor, raw: Tensor, tau: Tensor, M: Tensor, Z: Tensor, Nmax: Tensor,
+                scale: float, p: float, gamma: float, has_gamma: bool,
+                causal: bool) -> tuple[Tensor, Tensor]:
+    """Backward of pn_rows_fwd: (d_raw, dtau_rows) with dtau_rows[r] = -sum_j du[r, j]."""
+    N = raw.shape[-1]
+    r2 = raw.contiguous().view(-1, N)
+    g2 = dw.to(raw.dtype).contiguous().view(-1, N)
+    R = r2.shape[0]
+    d = torch.empty_like(r2)
+    dt = torch.empty(R, device=raw.device, dtype=torch.float32)
+    t32 = _tau32(tau)
+    rc = _lib.lib().pnfx_pn_rows_bwd(g2.data_ptr(), N, r2.data_ptr(), N, M.data_ptr(), Z.data_ptr(),
+                                     Nmax.data_ptr(), d.data_ptr(), N, dt.data_ptr(), R, N,
+                                     t32.data_ptr(), scale, p, gamma, int(has_gamma), int(causal),
+                                     _code(raw, "pn_rows"), _stream(raw))
+    _lib.check(rc, "pnfx_pn_rows_bwd")
+    return d.view(raw.shape), dt
+
+
+@pn_rows_bwd.register_fake
+def _(dw, raw, tau, M, Z, Nmax, scale, p, gamma, has_gamma, causal):
+    R = raw.numel() // max(raw.shape[-1], 1)
+    return torch.empty_like(raw), torch.empty(R, device=raw.device, dtype=torch.float32)
+
+
+def _rows_setup(ctx, inputs, output):
+    raw, tau, scale, p, gamma, has_gamma, causal = inputs
+    _, M, Z, Nm = output
+    ctx.save_for_backward(raw, tau, M, Z, Nm)
+    ctx.args = (scale, p, gamma, has_gamma, causal)
+
+
+def _rows_backward(ctx, dw, dM, dZ, dN):
+    raw, tau, M, Z, Nm = ctx.saved_tensors
+    d, dt = pn_rows_bwd(dw, raw, tau, M, Z, Nm, *ctx.args)
+    # fp64 sum of the row partials, as src/triton_pnfirtau.py:784
+    dtau = dt.sum(dtype=torch.float64).to(tau.dtype).view_as(tau)
+    return d, dtau, None, None, None, None, None
+
+
+torch.library.register_autograd("pnfx::pn_rows_fwd", _rows_backward, setup_context=_rows_setup)
+
+
+# ---------------------------------------------------------------------------- flash
+def _bhnd(t: Tensor, name: str, bf16: bool) -> Tensor:
+    """Return t with unit inner stride and (bf16) 16-byte-aligned, 8-element-multiple strides."""
+    if t.dim() != 4:
+        raise ValueError(f"{name} must be [B,H,N,D], got {tuple(t.shape)}")
+    ok = t.stride(-1) == 1
+    if ok and bf16:
+        ok = t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:3])
+    return t if ok else t.contiguous()
+
+
+@torch.library.custom_op("pnfx::flash_fwd", mutates_args=(), device_types="cuda")
+def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma: float,
+              has_gamma: bool, causal: bool,
+              o_bnhd: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Flash forward on [B,H,N,D]; returns (O, M, Z, Nmax, tile_mask).
+
+    O has shape [B,H,N,D]; with o_bnhd it is backed by a [B,N,H,D] buffer so that
+    the caller's transpose back to [B,N,H*D] is free.  tile_mask is uint8
+    [B*H, ceil(N/32), ceil(N/64)] (32-query x 64-key sub-tile activity).
+    """
+    B, H, N, D = q.shape
+    code = _code(q, "flash")
+    bf = code == _lib.PNFX_BF16
+    q, k, v = _bhnd(q, "q", bf), _bhnd(k, "k", bf), _bhnd(v, "v", bf)
+    if o_bnhd:
+        o = torch.empty((B, N, H, D), device=q.device, dtype=q.dtype).permute(0, 2, 1, 3)
+    else:
+        o = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
+    M = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
+    Z = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
+    Nm = torch.empty((B, H, N), device=q.device, dtype=torch.int32)
+    mask = torch.empty((B * H, (N + 31) // 32, (N + 63) // 64), device=q.device, dtype=torch.uint8)
+    t32 = _tau32(tau)
+    rc = _lib.lib().pnfx_flash_fwd(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        o.data_ptr(), o.stride(0), o.stride(1), o.stride(2),
+        M.data_ptr(), Z.data_ptr(), Nm.data_ptr(), mask.data_ptr(), B, H, N, D,
+        t32.data_ptr(), scale, gamma, int(has_gamma), int(causal), code, _stream(q))
+    _lib.check(rc, "pnfx_flash_fwd")
+    return o, M, Z, Nm, mask
+
+
+@flash_fwd.register_fake
+def _(q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd):
+    B, H, N, D = q.shape
+    if o_bnhd:
+        o = q.new_empty((B, N, H, D)).permute(0, 2, 1, 3)
+    else:
+        o = q.new_empty((B, H, N, D))
+    f = lambda dt: q.new_empty((B, H, N), dtype=dt)  # noqa: E731
+    mask = q.new_empty((B * H, (N + 31) // 32, (N + 63) // 64), dtype=torch.uint8)
+    return o, f(torch.float32), f(torch.float32), f(torch.int32), mask
+
+
+@torch.library.custom_op("pnfx::flash_bwd", mutates_args=(), device_types="cuda")
+def flash_bwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, o: Tensor, do: Tensor, M: Tensor,
+              Z: Tensor, Nmax: Tensor, mask: Tensor, scale: float, gamma: float, has_gamma: bool,
+              causal: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Deterministic flash backward; returns (dq, dk, dv, dtau) with dtau a 1-element fp32 tensor."""
+    B, H, N, D = q.shape
+    code = _code(q, "flash")
+    bf = code == _lib.PNFX_BF16
+    q, k, v = _bhnd(q, "q", bf), _bhnd(k, "k", bf), _bhnd(v, "v", bf)
+    o = _bhnd(o, "o", bf)
+    do = _bhnd(do.to(q.dtype), "dO", bf)
+    dq = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
+    dk = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
+    dv = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
+    dtau = torch.empty(1, device=q.device, dtype=torch.float32)
+    L = _lib.lib()
+    ws_bytes = L.pnfx_flash_bwd_workspace_size(B, H, N, D)
+    ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
+    t32 = _tau32(tau)
+    rc = L.pnfx_flash_bwd(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        o.data_ptr(), o.stride(0), o.stride(1), o.stride(2),
+        do.data_ptr(), do.stride(0), do.stride(1), do.stride(2),
+        M.data_ptr(), Z.data_ptr(), Nmax.data_ptr(), mask.data_ptr(),
+        dq.data_ptr(), dq.stride(0), dq.stride(1), dq.stride(2),
+        dk.data_ptr(), dk.stride(0), dk.stride(1), dk.stride(2),
+        dv.data_ptr(), dv.stride(0), dv.stride(1), dv.stride(2),
+        dtau.data_ptr(), ws.data_ptr(), ws_bytes, B, H, N, D,
+        t32.data_ptr(), scale, gamma, int(has_gamma), int(causal), code, _stream(q))
+    _lib.check(rc, "pnfx_flash_bwd")
+    return dq, dk, dv, dtau
+
+
+@flash_bwd.register_fake
+def _(q, k, v, tau, o, do, M, Z, Nmax, mask, scale, gamma, has_gamma, causal):
+    return (torch.empty_like(q, memory_format=torch.contiguous_format),
+            torch.empty_like(k, memory_format=torch.contiguous_format),
+            torch.empty_like(v, memory_format=torch.contiguous_format),
+            q.new_empty(1, dtype=torch.float32))
+
+
+def _flash_setup(ctx, inputs, output):
+    q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd = inputs
+    o, M, Z, Nm, mask = output
+    ctx.save_for_backward(q, k, v, tau, o, M, Z, Nm, mask)
+    ctx.args = (scale, gamma, has_gamma, causal)
+
+
+def _flash_backward(ctx, do, dM, dZ, dN, dmask):
+    q, k, v, tau, o, M, Z, Nm, mask = ctx.saved_tensors
+    dq, dk, dv, dt = flash_bwd(q, k, v, tau, o, do, M, Z, Nm, mask, *ctx.args)
+    return dq, dk, dv, dt.to(tau.dtype).view_as(tau), None, None, None, None, None
+
+
+torch.library.register_autograd("pnfx::flash_fwd", _flash_backward, setup_context=_flash_setup)

@@ -1,0 +1,134 @@
+"""GPU parity of the flash forward/backward against the float64 oracle.
+
+Tolerances (stated per the north-star contract): bf16 inputs -- every element within
+atol 2e-3 x max|ref| + rtol 2e-2 x |ref| of the oracle evaluated in float64 on the
+same bf16-rounded inputs; fp32 inputs -- 1e-5 on the same scale.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import pnfirtau_oracle as O
+from paper_01_anti_decoy_pnfirtau_amd.hip_pnfirtau import (flash_pn_fir_tau_attention,
+                                                           flash_pn_fir_tau_attention_with_stats,
+                                                           tile_mask_64)
+from tests.helpers import assert_close, flash_oracle, seeded, to_np64
+
+pytestmark = pytest.mark.gpu
+
+BF16_RTOL, BF16_ATOL = 2e-2, 2e-3
+F32_TOL = 1e-5
+
+
+def _run(q, k, v, tau_val, dO, scale, gamma, causal):
+    q = q.clone().requires_grad_(True)
+    k = k.clone().requires_grad_(True)
+    v = v.clone().requires_grad_(True)
+    tau = torch.tensor(tau_val, device=q.device, requires_grad=True)
+    o = flash_pn_fir_tau_attention(q, k, v, tau, scale=scale, gamma=gamma, causal_mask=causal)
+    o.backward(dO)
+    torch.cuda.synchronize()
+    return o, q.grad, k.grad, v.grad, tau.grad
+
+
+CASES = [
+    # B, H, N, D, tau, gamma, causal
+    (1, 2, 64, 64, 0.0, 0.5, True),
+    (2, 2, 200, 64, 0.0, 0.5, True),
+    (1, 3, 257, 64, 0.3, 0.5, True),
+    (2, 1, 130, 64, -0.2, None, True),
+    (1, 2, 96, 64, 0.1, 0.5, False),
+    (2, 2, 128, 16, 0.0, 0.5, True),
+    (1, 2, 100, 32, 0.2, 0.5, True),
+    (1, 2, 160, 128, 0.0, 0.5, True),
+    (1, 1, 1, 64, -0.5, 0.5, True),
+    (1, 1, 33, 16, 0.0, 0.75, False),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,H,N,D,tau,gamma,causal", CASES)
+def test_flash_matches_oracle(dev, dtype, B, H, N, D, tau, gamma, causal):
+    print(f"[flash B={B} H={H} N={N} D={D} tau={tau} gamma={gamma} causal={causal} {dtype}]", flush=True)
+    scale = 1.0 / np.sqrt(D)
+    q = seeded((B, H, N, D), 20, dtype, dev)
+    k = seeded((B, H, N, D), 21, dtype, dev)
+    v = seeded((B, H, N, D), 22, dtype, dev)
+    dO = seeded((B, H, N, D), 23, dtype, dev)
+    o, dq, dk, dv, dtau = _run(q, k, v, tau, dO, scale, gamma, causal)
+    Of, M, Z, Nm, rdq, rdk, rdv, rdt = flash_oracle(q, k, v, tau, dO, scale, gamma, causal)
+    if dtype == torch.bfloat16:
+        rt, at = BF16_RTOL, BF16_ATOL
+    else:
+        rt, at = F32_TOL, F32_TOL
+    assert_close(to_np64(o), Of, rt, at, "O")
+    assert_close(to_np64(dq), rdq, rt, at, "dq")
+    assert_close(to_np64(dk), rdk, rt, at, "dk")
+    assert_close(to_np64(dv), rdv, rt, at, "dv")
+    assert abs(float(dtau) - rdt) <= at * max(1.0, abs(rdt)) + rt * abs(rdt), (float(dtau), rdt)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_flash_stats_and_planted_ties(dev, dtype):
+    """Duplicate keys give exact score ties at the row peak: Nmax and the gate gradient split."""
+    B, H, N, D = 1, 2, 192, 64
+    q = seeded((B, H, N, D), 30, dtype, dev)
+    k = seeded((B, H, N, D), 31, dtype, dev)
+    k[:, :, 100] = k[:, :, 40]
+    k[:, :, 150] = k[:, :, 40]
+    q[:, :, 160:] = k[:, :, 40:41] * 2.0  # these rows peak on the triplicated key
+    v = seeded((B, H, N, D), 32, dtype, dev)
+    dO = seeded((B, H, N, D), 33, dtype, dev)
+    o, M, Z, Nm, mask = flash_pn_fir_tau_attention_with_stats(q, k, v, torch.tensor(0.0, device=dev))
+    Of, Mo, Zo, No, rdq, rdk, rdv, rdt = flash_oracle(q, k, v, 0.0, dO, 1 / 8, 0.5, True)
+    assert (No[:, :, 160:] == 3).all()
+    assert np.array_equal(Nm.cpu().numpy()[:, :, 160:], No[:, :, 160:])
+    np.testing.assert_allclose(M.cpu().numpy(), Mo, rtol=1e-2 if dtype == torch.bfloat16 else 1e-5)
+    _, dq, dk, dv, dtau = _run(q, k, v, 0.0, dO, 1 / 8, 0.5, True)
+    rt, at = (BF16_RTOL, BF16_ATOL) if dtype == torch.bfloat16 else (F32_TOL, F32_TOL)
+    assert_close(to_np64(dq), rdq, rt, at, "dq")
+    assert_close(to_np64(dk), rdk, rt, at, "dk")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_flash_tile_mask_planted_silent_blocks(dev, dtype):
+    """Zero key blocks at tau = 0.25 make exactly the planted 64x64 causal tiles silent."""
+    B, H, N, D = 1, 2, 1024, 64
+    q = seeded((B, H, N, D), 40, dtype, dev)
+    k = seeded((B, H, N, D), 41, dtype, dev)
+    v = seeded((B, H, N, D), 42, dtype, dev)
+    nb = N // 64
+    silent = [j for j in range(nb) if j % 2 == 0]
+    for j in silent:
+        k[:, :, 64 * j:64 * j + 64] = 0
+    tau = torch.tensor(0.25, device=dev)
+    o, M, Z, Nm, mask = flash_pn_fir_tau_attention_with_stats(q, k, v, tau)
+    act, amb = O.tile_activity(to_np64(q), to_np64(k), 0.25)
+    assert not amb.any()
+    m64 = tile_mask_64(mask).cpu().numpy().reshape(B, H, nb, nb).astype(bool)
+    assert np.array_equal(m64, act)
+    causal_tiles = nb * (nb + 1) // 2
+    assert (~act[0, 0]).sum() - (nb * nb - causal_tiles) == sum(nb - j for j in silent)
+
+
+def test_flash_backward_is_deterministic(dev):
+    B, H, N, D = 2, 2, 512, 64
+    q = seeded((B, H, N, D), 50, torch.bfloat16, dev)
+    k = seeded((B, H, N, D), 51, torch.bfloat16, dev)
+    v = seeded((B, H, N, D), 52, torch.bfloat16, dev)
+    dO = seeded((B, H, N, D), 53, torch.bfloat16, dev)
+    r1 = _run(q, k, v, 0.0, dO, 1 / 8, 0.5, True)
+    r2 = _run(q, k, v, 0.0, dO, 1 / 8, 0.5, True)
+    for a, b in zip(r1, r2):
+        assert torch.equal(a, b)
+
+
+def test_flash_strided_inputs_match_contiguous(dev):
+    """q, k, v as head views of a packed [B, N, 3, H, d] buffer (the qkv GEMM layout)."""
+    B, N, H, D = 2, 160, 4, 64
+    qkv = seeded((B, N, 3, H, D), 60, torch.bfloat16, dev)
+    q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+    tau = torch.tensor(0.0, device=dev)
+    o1 = flash_pn_fir_tau_attention(q, k, v, tau)
+    o2 = flash_pn_fir_tau_attention(q.contiguous(), k.contiguous(), v.contiguous(), tau)
+    assert torch.equal(o1, o2)

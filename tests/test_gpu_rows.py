@@ -1,0 +1,54 @@
+"""GPU parity of the row-fused score kernels against the oracle (src/triton_pnfirtau.py:141-303)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import pnfirtau_oracle as O
+from tests.helpers import assert_close, seeded, to_np64
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N,causal,p,gamma", [(24, True, 10.0, 0.5), (130, True, 10.0, 0.5),
+                                              (64, False, 2.0, None), (50, True, 3.5, 0.75),
+                                              (512, True, 10.0, 0.5), (5000, True, 10.0, 0.5)])
+def test_rows_fwd_bwd_match_oracle(dev, dtype, N, causal, p, gamma):
+    print(f"[rows N={N} causal={causal} p={p} gamma={gamma} {dtype}]", flush=True)
+    B, H = (2, 2) if N < 1000 else (1, 1)
+    raw = seeded((B, H, N, N), 10, dtype, dev, scale=3.0)
+    if N >= 24:
+        raw[0, 0, 20, :5] = raw[0, 0, 20, 7]  # planted tie at the row peak candidates
+    tau = torch.tensor(0.3, device=dev, requires_grad=True)
+    scale = 0.25
+    rawg = raw.clone().requires_grad_(True)
+    from paper_01_anti_decoy_pnfirtau_amd.hip_pnfirtau import hip_pn_fir_tau_scores
+    w = hip_pn_fir_tau_scores(rawg, tau, scale=scale, p=p, gamma=gamma, causal_mask=causal)
+    dW = seeded(w.shape, 11, dtype, dev)
+    w.backward(dW)
+    torch.cuda.synchronize()
+    rn = to_np64(raw)
+    W, M, Z, Nm = O.pn_rows_fwd(rn, 0.3, scale, p, gamma, causal)
+    d_raw, dtr = O.pn_rows_bwd(to_np64(dW), rn, 0.3, M, Z, Nm, scale, p, gamma, causal)
+    tol = 2e-5 if dtype == torch.float32 else 1e-2
+    assert_close(to_np64(w), W, tol, tol * 0.1, "W")
+    assert_close(to_np64(rawg.grad), d_raw, tol, tol * 0.1, "d_raw")
+    assert abs(float(tau.grad) - dtr.sum()) <= tol * max(1.0, np.abs(dtr).sum())
+
+
+def test_rows_stats_and_silent_rows(dev):
+    raw = seeded((1, 1, 40, 40), 12, torch.float32, dev)
+    raw[0, 0, 10] = -5.0  # silent row
+    raw[0, 0, 30, :4] = 3.0  # four-way tie at the peak
+    tau = torch.tensor(0.1, device=dev)
+    w, M, Z, Nm = torch.ops.pnfx.pn_rows_fwd(raw, tau, 1.0, 10.0, 0.5, True, True)
+    Wo, Mo, Zo, No = O.pn_rows_fwd(to_np64(raw), 0.1, 1.0, 10.0, 0.5, True)
+    assert np.array_equal(Nm.cpu().numpy(), No.reshape(-1))
+    assert float(M[10]) == 0.0 and float(Z[10]) == pytest.approx(1e-12) and int(Nm[10]) == 0
+    assert int(Nm[30]) == 4
+    assert torch.all(w[0, 0, 10] == 0)
+    np.testing.assert_allclose(M.cpu().numpy(), Mo.reshape(-1), rtol=1e-6)
+    np.testing.assert_allclose(Z.cpu().numpy(), Zo.reshape(-1), rtol=1e-5)
+    # row sums equal the gate
+    g = Mo / (Mo + 0.5)
+    np.testing.assert_allclose(w.sum(-1).cpu().numpy().reshape(-1), g.reshape(-1), rtol=1e-5, atol=1e-7)

@@ -1,0 +1,150 @@
+"""CPU-side tests of the product package: eager primitives against the reference's golden
+vectors, module drop-in properties, and the C ABI library surface (no GPU compute)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import paper_01_anti_decoy_pnfirtau_amd as P
+from paper_01_anti_decoy_pnfirtau_amd import _lib
+from tests.conftest import ROOT, golden
+
+
+def _t(a):
+    a = np.asarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+    return torch.from_numpy(np.ascontiguousarray(a))
+
+
+def test_taps_bit_exact_vs_reference_vector():
+    t = P.causal_gaussian_taps(7)
+    assert t.flip(0).tolist() == [0.33288270235061646, 0.2937679588794708, 0.2019035667181015,
+                                  0.10807118564844131, 0.04505077376961708, 0.014625845476984978,
+                                  0.003697992768138647]
+    f = golden("fir_eager")
+    assert P.causal_gaussian_taps(5, sigma_frac=2.0).tolist() == f["taps5"].tolist()
+
+
+def test_eager_fir_matches_reference_golden_bit_exact():
+    f = golden("fir_eager")
+    taps = _t(f["taps"])
+    assert torch.equal(P.causal_fir(_t(f["x"]), taps), _t(f["y_f32"]))
+    yb = P.causal_fir(_t(f["x_bf16"]), taps)
+    assert torch.equal(yb.view(torch.int16), _t(f["y_bf16"]).view(torch.int16))
+
+
+@pytest.mark.parametrize("i", range(8))
+def test_eager_power_norm_matches_reference_golden(i):
+    f = golden("pn_gate")
+    p, g, m = str(f["cases"][i]).split("|")
+    s = _t(f["s"]).clone().requires_grad_(True)
+    w = P.power_norm_peak_gate(s, float(p), None if g == "None" else float(g), m)
+    w.backward(_t(f["dW"]))
+    assert torch.equal(w.detach(), _t(f[f"w_{i}"]))
+    assert torch.allclose(s.grad, _t(f[f"ds_{i}"]), rtol=0, atol=1e-15)
+
+
+def test_unknown_silence_mode_raises():
+    with pytest.raises(ValueError):
+        P.power_norm_peak_gate(torch.randn(2, 4), silence_mode="nope")
+
+
+def test_cpu_row_scores_follow_reference_fallback():
+    from paper_01_anti_decoy_pnfirtau_amd.hip_pnfirtau import triton_pn_fir_tau_scores
+
+    f = golden("scores_fallback")
+    raw, tau = _t(f["raw"]), _t(f["tau"])
+    for i in range(3):
+        scale, p, g, causal = f[f"args_{i}"]
+        w = triton_pn_fir_tau_scores(raw, tau, scale=float(scale), p=float(p),
+                                     gamma=None if np.isnan(g) else float(g), causal_mask=bool(causal))
+        assert torch.equal(w, _t(f[f"w_{i}"]))
+
+
+def _load_mha(cls, f, dtype=torch.float32):
+    B, N, D, H, bias = [int(x) for x in f["meta"]]
+    g = float(f["gamma"])
+    cfg = P.PnFirConfig(d_model=D, n_heads=H, p=float(f["p"]), silence_gamma=None if np.isnan(g) else g,
+                        silence_mode=str(f["mode"]), bias=bool(bias))
+    m = cls(cfg)
+    sd = {"qkv.weight": _t(f["w_qkv"]), "out.weight": _t(f["w_out"]),
+          "score_tau": _t(f["tau"]).reshape(()).float(), "fir_taps": _t(f["taps"]).float()}
+    if bias:
+        sd.update({"qkv.bias": _t(f["b_qkv"]), "out.bias": _t(f["b_out"])})
+    m.load_state_dict(sd)
+    return m.to(dtype)
+
+
+@pytest.mark.parametrize("name", ["c1_mha_fp32", "c1_mha_fp32_tau", "c1_mha_fp32_bias_modes", "c1_mha_fp32_nogate"])
+def test_eager_mha_matches_reference_golden(name):
+    f = golden(name)
+    m = _load_mha(P.PnFirTauMHA, f)
+    x = _t(f["x"]).clone().requires_grad_(True)
+    out, W = m(x, return_weights=True)
+    out.backward(_t(f["dout"]))
+    assert torch.allclose(out, _t(f["out"]), rtol=0, atol=1e-6)
+    assert torch.allclose(x.grad, _t(f["dx"]), rtol=0, atol=1e-5)
+    assert torch.allclose(m.qkv.weight.grad, _t(f["dw_qkv"]), rtol=0, atol=1e-4)
+    assert torch.allclose(m.out.weight.grad, _t(f["dw_out"]), rtol=0, atol=1e-4)
+    assert abs(float(m.score_tau.grad) - float(f["dtau"])) <= 1e-6 * max(1.0, abs(float(f["dtau"])))
+
+
+def test_state_dict_keys_and_subclassing_match_reference():
+    cfg = P.PnFirConfig()
+    for cls in (P.PnFirTauMHA, P.PnFirTauTritonMHA, P.PnFirTauFlashMHA):
+        m = cls(cfg)
+        assert list(m.state_dict().keys()) == ["score_tau", "fir_taps", "qkv.weight", "out.weight"]
+        assert isinstance(m, P.PnFirTauMHA)
+        assert m.score_tau.shape == () and m.fir_taps.shape == (7,)
+    mb = P.PnFirTauMHA(P.PnFirConfig(bias=True))
+    assert set(mb.state_dict()) == {"score_tau", "qkv.weight", "qkv.bias", "out.weight", "out.bias", "fir_taps"}
+
+
+def test_default_init_consumes_rng_like_reference():
+    f = golden("c1_mha_fp32")
+    torch.manual_seed(0)
+    m = P.PnFirTauMHA(P.PnFirConfig(d_model=64, n_heads=4, dropout=0.0))
+    assert torch.equal(m.qkv.weight.detach(), _t(f["w_qkv"]))
+    assert torch.equal(m.out.weight.detach(), _t(f["w_out"]))
+
+
+def _header_symbols():
+    txt = open(os.path.join(ROOT, "include", "pnfx.h")).read()
+    return sorted(set(re.findall(r"\b(pnfx_\w+)\s*\(", txt)))
+
+
+def test_c_abi_library_exports_every_declared_symbol():
+    syms = _header_symbols()
+    assert syms == sorted(_lib.exported_symbols())
+    lib = _lib.lib()
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert lib.pnfx_abi_version() == 1
+
+
+def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
+    lib = _lib.lib()
+    rc = lib.pnfx_flash_fwd(*([None, 0, 0, 0] * 4), None, None, None, None, 1, 1, 8, 48, None,
+                            0.125, 0.5, 1, 1, 1, None)
+    assert rc == -1 and b"head dim" in lib.pnfx_last_error()
+    rc = lib.pnfx_fir_fwd(None, 0, 0, 0, None, 1, 1, 4, 8, None, 1, 7, 1, None)
+    assert rc == -1 and b"null" in lib.pnfx_last_error()
+    rc = lib.pnfx_fir_fwd(ctypes.c_void_p(16), 0, 0, 0, ctypes.c_void_p(16), 1, 1, 4, 8,
+                          ctypes.c_void_p(16), 1, 17, 1, None)
+    assert rc == -1 and b"K=17" in lib.pnfx_last_error()
+    need = lib.pnfx_flash_bwd_workspace_size(4, 16, 8192, 64)
+    assert need >= 4 * 16 * 8192 * 32
+
+
+def test_hip_ops_refuse_cpu_tensors():
+    from paper_01_anti_decoy_pnfirtau_amd import ops  # noqa: F401
+
+    q = torch.randn(1, 1, 8, 16)
+    with pytest.raises(Exception):
+        torch.ops.pnfx.flash_fwd(q, q, q, torch.tensor(0.0), 0.25, 0.5, True, True, False)
+    with pytest.raises(RuntimeError):
+        P.flash_pn_fir_tau_attention(q, q, q, torch.tensor(0.0))
