@@ -1,0 +1,300 @@
+"""Throughput of the pn_fir_tau hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one flash pn_fir_tau forward + backward (autograd, as the reference's
+``kern1`` harness, experiments/exp4_wikitext2_lm.py:549-570) over one batch of
+config C4: B=4, H=16, N=8192, d_head=64, bf16, Q/K/V/dO ~ N(0,1), tau = 0, all
+inputs resident in HBM before the timed region.  ``value`` is algorithmic
+TFLOP/s, 7*B*H*N^2*d FLOP per step (forward 2 and backward 5 causal GEMMs).
+
+Also measured in the same run and reported on the same JSON line:
+* ``roofline``: the dominant kernel's algorithmic FLOP per launch over its
+  average duration from HIP events on the launch stream;
+* ``silent_50``: the same step with 50 % of the 8256 causal 64x64 tiles planted
+  silent (zero key blocks {even j} \\ {96}, tau = 0.25) and the speedup;
+* ``fir``: standalone causal FIR (config C2, K [8,8,2048,64] bf16, per-head
+  taps) in GB/s, rotating 20 input/output buffer pairs (640 MiB) so the 256 MB
+  Infinity Cache cannot serve repeats;
+* ``wide_head``: config C5 (B=8, H=8, N=4096, d=128) TFLOP/s;
+* ``cpu_baseline``: the numpy oracle (float32) forward + backward on one (b, h)
+  slice of C4 on this host's cores.
+
+``--only flash|fir|copy`` runs a single short workload (for rocprofv3 passes).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+METRIC = "pn_fir_tau flash fwd+bwd TFLOP/s (%MFMA peak) N=8192 d64 bf16; FIR GB/s"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
+C4 = dict(B=4, H=16, N=8192, D=64)
+C5 = dict(B=8, H=8, N=4096, D=128)
+
+
+def gemm_flops(B, H, N, D):
+    """One causal attention GEMM (N^2/2 pairs x d x 2 FLOP) over all heads."""
+    return B * H * N * N * D
+
+
+def make_inputs(B, H, N, D, seed, dev, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return [(torch.randn(B, H, N, D, generator=g) * std).to(torch.bfloat16).to(dev) for _ in range(4)]
+
+
+def plant_silent(k, N):
+    """Zero key blocks {even j} \\ {96}: with tau = 0.25 exactly half the causal 64x64 tiles are silent."""
+    nb = N // 64
+    silent = [j for j in range(nb) if j % 2 == 0 and j != 96]
+    for j in silent:
+        k[:, :, 64 * j:64 * j + 64] = 0
+    frac = sum(nb - j for j in silent) / (nb * (nb + 1) / 2)
+    return frac
+
+
+def time_steps(step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps * 1e3
+    return wall, ev0.elapsed_time(ev1) / steps
+
+
+def flash_step_fn(q, k, v, dO, tau_val):
+    from paper_01_anti_decoy_pnfirtau_amd.hip_pnfirtau import flash_pn_fir_tau_attention
+
+    q, k, v = (t.detach().requires_grad_(True) for t in (q, k, v))
+    tau = torch.tensor(tau_val, device=q.device, requires_grad=True)
+
+    def step():
+        for t in (q, k, v, tau):
+            t.grad = None
+        o = flash_pn_fir_tau_attention(q, k, v, tau)
+        o.backward(dO)
+
+    return step
+
+
+def kernel_times(q, k, v, dO, tau_val, iters):
+    """Average duration of each flash kernel stage from HIP events on the launch stream."""
+    from paper_01_anti_decoy_pnfirtau_amd import _lib, ops
+
+    L = _lib.lib()
+    B, H, N, D = q.shape
+    tau = torch.tensor(tau_val, device=q.device)
+    scale, gamma = 1.0 / math.sqrt(D), 0.5
+    o, o_lo, M, Z, Nm, mask = ops.flash_fwd(q, k, v, tau, scale, gamma, True, True, False)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    dtau = torch.empty(1, device=q.device)
+    wsb = L.pnfx_flash_bwd_workspace_size(B, H, N, D)
+    ws = torch.empty(wsb, device=q.device, dtype=torch.uint8)
+    t32 = tau.reshape(1).float()
+    st = torch.cuda.current_stream().cuda_stream
+
+    def bwd(stages):
+        rc = L.pnfx_flash_bwd_stages(
+            stages, *ops._ptr4(q), *ops._ptr4(k), *ops._ptr4(v), *ops._ptr4(o), o_lo.data_ptr(),
+            *ops._ptr4(dO), M.data_ptr(), Z.data_ptr(), Nm.data_ptr(), mask.data_ptr(),
+            *ops._ptr4(dq), *ops._ptr4(dk), *ops._ptr4(dv), dtau.data_ptr(), ws.data_ptr(), wsb,
+            B, H, N, D, t32.data_ptr(), scale, gamma, 1, 1, _lib.PNFX_BF16, st)
+        _lib.check(rc, "pnfx_flash_bwd_stages")
+
+    stages = {
+        "flash_fwd_kernel": lambda: ops.flash_fwd(q, k, v, tau, scale, gamma, True, True, False),
+        "flash_bwd_pre_kernel": lambda: bwd(_lib.PNFX_BWD_PREPARE),
+        "flash_bwd_dkdv_kernel": lambda: bwd(_lib.PNFX_BWD_DKDV),
+        "flash_bwd_dq_kernel": lambda: bwd(_lib.PNFX_BWD_DQ),
+    }
+    gf = gemm_flops(B, H, N, D)
+    alg = {"flash_fwd_kernel": 2 * gf, "flash_bwd_pre_kernel": 0,
+           "flash_bwd_dkdv_kernel": 4 * gf, "flash_bwd_dq_kernel": 1 * gf}
+    out = {}
+    for name, fn in stages.items():
+        fn()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+        for e0, e1 in evs:
+            e0.record()
+            fn()
+            e1.record()
+        torch.cuda.synchronize()
+        ms = sum(e0.elapsed_time(e1) for e0, e1 in evs) / iters
+        out[name] = {"ms": round(ms, 4), "alg_tflop": alg[name] / 1e12,
+                     "tflops": round(alg[name] / (ms * 1e-3) / 1e12, 2) if alg[name] else None}
+    return out
+
+
+def bench_fir(dev, reps=200, pairs=20):
+    from paper_01_anti_decoy_pnfirtau_amd import ops  # noqa: F401
+
+    g = torch.Generator().manual_seed(7)
+    xs = [torch.randn(8, 8, 2048, 64, generator=g).to(torch.bfloat16).to(dev) for _ in range(pairs)]
+    ys = [torch.empty_like(x) for x in xs]
+    t = torch.rand(8, 7, generator=g)
+    taps = (t / t.sum(-1, keepdim=True)).to(dev)
+    from paper_01_anti_decoy_pnfirtau_amd import _lib
+
+    L = _lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+
+    def launch(i):
+        x, y = xs[i % pairs], ys[i % pairs]
+        rc = L.pnfx_fir_fwd(x.data_ptr(), x.stride(0), x.stride(1), x.stride(2), y.data_ptr(),
+                            8, 8, 2048, 64, taps.data_ptr(), 8, 7, _lib.PNFX_BF16, st)
+        _lib.check(rc, "pnfx_fir_fwd")
+
+    for i in range(pairs):
+        launch(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        launch(i)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / reps * 1e3
+    nbytes = 2 * 8 * 8 * 2048 * 64 * 2
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"us_per_launch": round(us, 3), "bytes": nbytes, "gbps": round(gbps, 1),
+            "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4), "buffers": f"{pairs} pairs x 32 MiB"}
+
+
+def bench_copy(dev, mib=512, reps=20):
+    """A plain device copy of known size: the calibration point for FETCH_SIZE / WRITE_SIZE."""
+    a = torch.empty(mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return {"copy_bytes_each_way": mib << 20, "reps": reps}
+
+
+def cpu_baseline(slices=8):
+    """numpy oracle (float32) forward + backward on `slices` (b, h) slices of C4."""
+    import numpy as np
+
+    from oracle import pnfirtau_oracle as O
+
+    N, D = C4["N"], C4["D"]
+    rng = np.random.default_rng(0)
+    dt = 0.0
+    for _ in range(slices):
+        q, k, v, dO = (rng.standard_normal((1, 1, N, D)).astype(np.float32) for _ in range(4))
+        t0 = time.perf_counter()
+        O.flash_fwd(q, k, v, 0.0, dtype=np.float32)
+        O.flash_bwd(q, k, v, 0.0, dO, dtype=np.float32)
+        dt += time.perf_counter() - t0
+    flops = 7 * N * N * D * slices
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{slices} (b,h) slices of C4 (N={N}, d={D}) fwd+bwd, numpy float32 oracle, "
+                      f"{dt:.2f} s; BLAS on {threads} threads, elementwise on 1"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=["flash", "fir", "copy"], default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
+              file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    import paper_01_anti_decoy_pnfirtau_amd.hip_pnfirtau  # noqa: F401  (loads libpnfx.so)
+
+    if args.only == "copy":
+        print(json.dumps(bench_copy(dev)))
+        return
+    if args.only == "fir":
+        print(json.dumps(bench_fir(dev, reps=50)))
+        return
+
+    B, H, N, D = C4["B"], C4["H"], C4["N"], C4["D"]
+    flops = 7 * gemm_flops(B, H, N, D)
+    q, k, v, dO = make_inputs(B, H, N, D, 0, dev)
+    step = flash_step_fn(q, k, v, dO, 0.0)
+    wall_ms, ev_ms = time_steps(step, args.steps, args.warmup)
+    if args.only == "flash":
+        print(json.dumps({"ms_per_step": wall_ms, "event_ms": ev_ms}))
+        return
+    kern = kernel_times(q, k, v, dO, 0.0, max(5, args.steps // 2))
+    dom = max((n for n in kern if kern[n]["tflops"]), key=lambda n: kern[n]["ms"])
+    achieved = kern[dom]["tflops"]
+
+    # 50 % silent tiles
+    ks = k.clone()
+    frac = plant_silent(ks, N)
+    step_s = flash_step_fn(q, ks, v, dO, 0.25)
+    wall_s, ev_s = time_steps(step_s, args.steps, args.warmup)
+    del step_s, ks
+
+    fir = bench_fir(dev)
+
+    # C5 wide heads, Q/K/V ~ N(0, 1/sqrt(d))
+    B5, H5, N5, D5 = C5["B"], C5["H"], C5["N"], C5["D"]
+    q5, k5, v5, dO5 = make_inputs(B5, H5, N5, D5, 1, dev, std=D5 ** -0.25)
+    wall5, ev5 = time_steps(flash_step_fn(q5, k5, v5, dO5, 0.0), max(3, args.steps // 2), 2)
+    flops5 = 7 * gemm_flops(B5, H5, N5, D5)
+    del q5, k5, v5, dO5
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
+
+    value = flops / (wall_ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "C4 flash pn_fir_tau fwd+bwd (autograd step)", "B": B, "H": H,
+                   "N": N, "d_head": D, "tau": 0.0, "gamma": 0.5, "causal": True,
+                   "silent_tile_fraction": 0.0, "alg_tflop_per_step": round(flops / 1e12, 4)},
+        "frac_mfma_peak": round(value / PEAK_BF16_TFLOPS, 4),
+        "event_ms_per_step": round(ev_ms, 4),
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved,
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "kernels": kern,
+        "silent_50": {"silent_fraction": round(frac, 4), "tau": 0.25,
+                      "ms_per_step": round(wall_s, 4), "event_ms_per_step": round(ev_s, 4),
+                      "speedup": round(wall_ms / wall_s, 3)},
+        "fir": fir,
+        "wide_head": {"config": C5, "ms_per_step": round(wall5, 4),
+                      "tflops": round(flops5 / (wall5 * 1e-3) / 1e12, 2)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -97,6 +97,9 @@ int pnfx_pn_rows_bwd(const void* dw, int64_t dw_rs, const void* raw, int64_t raw
 /*
  * Flash pn_fir_tau attention forward (p = 10, peak gate), O(N) memory.
  *   q, k, v, o : [B, H, N, D] with strides (s?b, s?h, s?n, 1), same dtype
+ *   o_lo       : optional (may be NULL; bf16 only), o's strides: the bf16 rounding
+ *                residual of O (fp32 O = o + o_lo to ~16 mantissa bits), which
+ *                pnfx_flash_bwd uses to form D = <dO, O>/gate accurately
  *   M, Z       : fp32 [B, H, N] contiguous; Nmax: int32 [B, H, N] contiguous
  *   tile_mask  : optional (may be NULL) uint8 [B*H, ceil(N/32), ceil(N/64)]:
  *                1 where the 32-query x 64-key sub-tile has a positive
@@ -108,7 +111,8 @@ int pnfx_pn_rows_bwd(const void* dw, int64_t dw_rs, const void* raw, int64_t raw
 int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
                    int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
                    int64_t vsh, int64_t vsn, void* o, int64_t osb, int64_t osh, int64_t osn,
-                   float* M, float* Z, int32_t* Nmax, uint8_t* tile_mask, int64_t B, int64_t H,
+                   void* o_lo, float* M, float* Z, int32_t* Nmax, uint8_t* tile_mask, int64_t B,
+                   int64_t H,
                    int64_t N, int64_t D, const float* tau, float scale, float gamma,
                    int has_gamma, int causal, int dtype, void* stream);
 
@@ -116,8 +120,9 @@ int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const v
 int64_t pnfx_flash_bwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D);
 
 /*
- * Flash backward.  Inputs as saved by the forward (q, k, v, o, M, Z, Nmax,
- * tile_mask -- tile_mask may be NULL, then every causal tile is recomputed),
+ * Flash backward.  Inputs as saved by the forward (q, k, v, o, o_lo, M, Z, Nmax,
+ * tile_mask -- o_lo and tile_mask may be NULL; without tile_mask every causal
+ * tile is recomputed),
  * dO with its own strides.  Outputs dq, dk, dv ([B,H,N,D] with their own
  * strides, dtype of q) and dtau (one fp32: the fp64 sum of all per-tile
  * partials rounded once, as src/triton_pnfirtau.py:959).  Deterministic: no
@@ -129,7 +134,7 @@ int64_t pnfx_flash_bwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D
 int pnfx_flash_bwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
                    int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
                    int64_t vsh, int64_t vsn, const void* o, int64_t osb, int64_t osh,
-                   int64_t osn, const void* dout, int64_t dosb, int64_t dosh, int64_t dosn,
+                   int64_t osn, const void* o_lo, const void* dout, int64_t dosb, int64_t dosh, int64_t dosn,
                    const float* M, const float* Z, const int32_t* Nmax,
                    const uint8_t* tile_mask, void* dq, int64_t dqsb, int64_t dqsh,
                    int64_t dqsn, void* dk, int64_t dksb, int64_t dksh, int64_t dksn, void* dv,
@@ -137,6 +142,30 @@ int pnfx_flash_bwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const v
                    int64_t workspace_bytes, int64_t B, int64_t H, int64_t N, int64_t D,
                    const float* tau, float scale, float gamma, int has_gamma, int causal,
                    int dtype, void* stream);
+
+/*
+ * The three stages of pnfx_flash_bwd, callable separately (same arguments,
+ * plus a stage mask): PNFX_BWD_PREPARE forms the per-row constants in the
+ * workspace; PNFX_BWD_DKDV writes dk, dv and dtau; PNFX_BWD_DQ writes dq.
+ * DKDV and DQ each depend only on PREPARE, so a caller may run them on two
+ * streams after an event; pnfx_flash_bwd is the mask PNFX_BWD_ALL on one stream.
+ */
+#define PNFX_BWD_PREPARE 1
+#define PNFX_BWD_DKDV 2
+#define PNFX_BWD_DQ 4
+#define PNFX_BWD_ALL 7
+int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int64_t qsh, int64_t qsn,
+                          const void* k, int64_t ksb, int64_t ksh, int64_t ksn, const void* v,
+                          int64_t vsb, int64_t vsh, int64_t vsn, const void* o, int64_t osb,
+                          int64_t osh, int64_t osn, const void* o_lo, const void* dout,
+                          int64_t dosb, int64_t dosh, int64_t dosn, const float* M,
+                          const float* Z, const int32_t* Nmax, const uint8_t* tile_mask,
+                          void* dq, int64_t dqsb, int64_t dqsh, int64_t dqsn, void* dk,
+                          int64_t dksb, int64_t dksh, int64_t dksn, void* dv, int64_t dvsb,
+                          int64_t dvsh, int64_t dvsn, float* dtau, void* workspace,
+                          int64_t workspace_bytes, int64_t B, int64_t H, int64_t N, int64_t D,
+                          const float* tau, float scale, float gamma, int has_gamma, int causal,
+                          int dtype, void* stream);
 
 #ifdef __cplusplus
 }

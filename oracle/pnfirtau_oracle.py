@@ -384,7 +384,8 @@ def flash_fwd(q, k, v, tau, scale=None, gamma=0.5, causal=True, dtype=np.float64
     return O, M, Z, nmax
 
 
-def flash_bwd(q, k, v, tau, dO, scale=None, gamma=0.5, causal=True):
+def flash_bwd(q, k, v, tau, dO, scale=None, gamma=0.5, causal=True, return_abs=False,
+              dtype=np.float64):
     """Flash backward semantics, float64: returns (dq, dk, dv, dtau).
 
     Recomputes u from q, k; w = u^10 g/Z; dv = w^T dO; dW = dO v^T;
@@ -393,14 +394,14 @@ def flash_bwd(q, k, v, tau, dO, scale=None, gamma=0.5, causal=True):
     dS = du*scale; dq = dS k; dk = dS^T q; dtau = -sum du
     (src/triton_pnfirtau.py:530-602, :959).
     """
-    q = np.asarray(q, dtype=np.float64)
-    k = np.asarray(k, dtype=np.float64)
-    v = np.asarray(v, dtype=np.float64)
-    dO = np.asarray(dO, dtype=np.float64)
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    v = np.asarray(v, dtype=dtype)
+    dO = np.asarray(dO, dtype=dtype)
     if scale is None:
         scale = 1.0 / np.sqrt(q.shape[-1])
-    s, valid = _flash_scores(q, k, tau, scale, causal, np.float64)
-    u = np.where(valid & (s > 0), s, 0.0)
+    s, valid = _flash_scores(q, k, tau, scale, causal, dtype)
+    u = np.where(valid & (s > 0), s, dtype(0))
     P = _pow_p(u, 10.0)
     Z = (P.sum(axis=-1) + EPS_Z)[..., None]
     M = u.max(axis=-1)[..., None]
@@ -419,6 +420,8 @@ def flash_bwd(q, k, v, tau, dO, scale=None, gamma=0.5, causal=True):
     dS = du * scale
     dq = np.matmul(dS, k)
     dk = np.matmul(np.swapaxes(dS, -1, -2), q)
+    if return_abs:  # sum |du|: the conditioning scale of the dtau sum
+        return dq, dk, dv, -du.sum(), np.abs(du).sum()
     return dq, dk, dv, -du.sum()
 
 
@@ -510,6 +513,7 @@ def mha_fwd_bwd(x, w_qkv, w_out, tau, taps, n_heads, dout=None, b_qkv=None, b_ou
     ds = power_norm_peak_gate_bwd(s, dWt, p, gamma, silence_mode)
     ds = np.where(masked, 0.0, ds)
     res["dtau"] = -ds.sum()
+    res["dtau_abs"] = np.abs(ds).sum()
     draw = ds * scale
     dq = np.matmul(draw, k)
     dk = np.matmul(np.swapaxes(draw, -1, -2), q)

@@ -8,6 +8,7 @@ namespace pnfx {
 struct FwdParams {
   const void *q, *k, *v;
   void* o;
+  void* o_lo;  // optional bf16 rounding residual of O (same strides as o)
   int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
   float* M;
   float* Z;
@@ -19,7 +20,7 @@ struct FwdParams {
 };
 
 struct BwdParams {
-  const void *q, *k, *v, *o, *dout;
+  const void *q, *k, *v, *o, *o_lo, *dout;
   void *dq, *dk, *dv;
   int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn, dosb, dosh, dosn;
   int64_t dqsb, dqsh, dqsn, dksb, dksh, dksn, dvsb, dvsh, dvsn;
@@ -28,7 +29,7 @@ struct BwdParams {
   const int32_t* Nmax;
   const uint8_t* mask;
   float* rc;        // row constants [B*H*N][8]: M, r = g/Z, c = 10 g/Z * scale, Dv, G
-  float* partials;  // tau partials [B*H][nkvb][4]
+  double* partials;  // tau partials [B*H][nkvb][4]
   float* dtau;
   int B, H, N, nq32, nk64, nkvb;
   const float* tau;
@@ -43,8 +44,10 @@ inline int bwd_nkvb(int64_t N, int64_t D) {
 int64_t bwd_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D);
 
 int flash_fwd_bf16(const FwdParams& fp, int64_t D, bool causal, bool has_gamma, hipStream_t st);
-int flash_bwd_bf16(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, hipStream_t st);
+int flash_bwd_bf16(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, int stages,
+                   hipStream_t st);
 int flash_fwd_f32(const FwdParams& fp, int64_t D, bool causal, bool has_gamma, hipStream_t st);
-int flash_bwd_f32(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, hipStream_t st);
+int flash_bwd_f32(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, int stages,
+                  hipStream_t st);
 
 }  // namespace pnfx

@@ -2,14 +2,14 @@
 //
 // Math (src/triton_pnfirtau.py:313-621): per query row i and key j <= i,
 //   s = fma(q_i . k_j, scale, -tau), u = relu(s), P = u^10 (four multiplies, no exp),
-//   mass += P, peak = max u, Nmax = #(u == peak);
+//   mass += bf16(P), peak = max u, Nmax = #(u == peak);
 //   O_i = (sum_j bf16(P_ij) v_j) * gate_i / (mass_i + 1e-12), gate = peak/(peak + gamma).
 // There is no running rescale (unlike softmax), so mass and peak stay lane-local for the
 // whole key loop and are reduced across lanes once, in the epilogue.
 //
 // MFMA mapping: v_mfma_f32_16x16x32_bf16.  The forward and the dQ kernel compute S^T =
 // K Q^T, whose C layout gives each lane one query row (lane % 16) and four keys per 16-key
-// block.  The key order of the K fragment is permuted (key_of below) so that the 8 keys a
+// block.  The key order of the K fragment is permuted (perm_row below) so that the 8 keys a
 // lane group holds after two blocks are contiguous: the C registers then feed the next
 // MFMA (P^T or dS^T as its B operand) directly, and the A operand (V^T or K^T) is one
 // 16-byte LDS read from a transposed tile.  The dK/dV kernel computes S = Q K^T with the
@@ -136,7 +136,17 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) acc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float mrun[2] = {0.f, 0.f}, mass[2] = {0.f, 0.f};
+  // The power mass is accumulated by the MFMA as one extra "dimension" of V whose value is
+  // 1: a constant A fragment with ones in row 0.  The mass is then the sum of exactly the
+  // bf16-rounded P that weights V, so O = gate * sum(P v) / sum(P) is a true convex
+  // combination and the flash identity D = <dO, O>/gate holds for the P actually used.
+  f32x4 accm[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  bf16x8 ones = zero_bf16x8();
+  if (r16 == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (bf16)1.0f;
+  }
+  float mrun[2] = {0.f, 0.f};
   int cnt[2] = {0, 0};
 
   const int kv_end = CAUSAL ? min(m0 + BM, N) : N;
@@ -204,16 +214,10 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
             for (int i = 0; i < 4; ++i) c += (s[kb][qb][i] == mnew) ? 1 : 0;
           cnt[qb] = c;
           mrun[qb] = mnew;
-          float ms = mass[qb];
 #pragma unroll
           for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float pw = pow10f_(s[kb][qb][i]);
-              ms += pw;
-              s[kb][qb][i] = pw;
-            }
-          mass[qb] = ms;
+            for (int i = 0; i < 4; ++i) s[kb][qb][i] = pow10f_(s[kb][qb][i]);
         }
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) {
@@ -229,6 +233,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(vf, pf[qb], acc[db][qb]);
           }
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) accm[qb] = mfma16x16x32(ones, pf[qb], accm[qb]);
         }
       }
     }
@@ -239,6 +245,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
 
   // Epilogue: reduce the lane-local statistics over the four lane groups of a row.
   bf16* O = static_cast<bf16*>(p.o) + b * p.osb + h * p.osh;
+  bf16* Olo = p.o_lo ? static_cast<bf16*>(p.o_lo) + b * p.osb + h * p.osh : nullptr;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const float m = mrun[qb];
@@ -247,9 +254,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
     int c = (m == Mx) ? cnt[qb] : 0;
     c += __shfl_xor(c, 16, 64);
     c += __shfl_xor(c, 32, 64);
-    float ms = mass[qb];
-    ms += __shfl_xor(ms, 16, 64);
-    ms += __shfl_xor(ms, 32, 64);
+    // row 0 of the mass block lives in lane r16 (lane group 0), register 0
+    const float ms = __shfl(accm[qb][0], r16, 64);
     const float gate = Mx > 0.f ? (HAS_GAMMA ? Mx / (Mx + p.gamma) : 1.f) : 0.f;
     const float z = ms + 1e-12f;
     const float so = gate / z;
@@ -257,10 +263,16 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
     if (qrow < N) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        bf16x4 o4;
+        bf16x4 o4, r4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o4[i] = (bf16)(acc[db][qb][i] * so);
-        *reinterpret_cast<bf16x4*>(O + (int64_t)qrow * p.osn + 16 * db + 4 * g) = o4;
+        for (int i = 0; i < 4; ++i) {
+          const float of = acc[db][qb][i] * so;
+          o4[i] = (bf16)of;
+          r4[i] = (bf16)(of - (float)o4[i]);
+        }
+        const int64_t off = (int64_t)qrow * p.osn + 16 * db + 4 * g;
+        *reinterpret_cast<bf16x4*>(O + off) = o4;
+        if (Olo) *reinterpret_cast<bf16x4*>(Olo + off) = r4;
       }
       if (g == 0) {
         const int64_t si = (int64_t)bh * N + qrow;
@@ -289,13 +301,18 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
     bh = row / p.N;
     i = row % p.N;
     const int64_t b = bh / p.H, h = bh % p.H;
-    const u32x4 ov = *reinterpret_cast<const u32x4*>(static_cast<const bf16*>(p.o) + b * p.osb + h * p.osh + i * p.osn + 8 * part);
+    const int64_t ooff = b * p.osb + h * p.osh + i * p.osn + 8 * part;
+    const u32x4 ov = *reinterpret_cast<const u32x4*>(static_cast<const bf16*>(p.o) + ooff);
+    u32x4 lv = {0u, 0u, 0u, 0u};
+    if (p.o_lo) lv = *reinterpret_cast<const u32x4*>(static_cast<const bf16*>(p.o_lo) + ooff);
     const u32x4 dv =
         *reinterpret_cast<const u32x4*>(static_cast<const bf16*>(p.dout) + b * p.dosb + h * p.dosh + i * p.dosn + 8 * part);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      dot = __builtin_fmaf(__uint_as_float(ov[e] << 16), __uint_as_float(dv[e] << 16), dot);
-      dot = __builtin_fmaf(__uint_as_float(ov[e] & 0xffff0000u), __uint_as_float(dv[e] & 0xffff0000u), dot);
+      const float o0 = __uint_as_float(ov[e] << 16) + __uint_as_float(lv[e] << 16);
+      const float o1 = __uint_as_float(ov[e] & 0xffff0000u) + __uint_as_float(lv[e] & 0xffff0000u);
+      dot = __builtin_fmaf(o0, __uint_as_float(dv[e] << 16), dot);
+      dot = __builtin_fmaf(o1, __uint_as_float(dv[e] & 0xffff0000u), dot);
     }
   }
 #pragma unroll
@@ -526,7 +543,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
       adk[db][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
       adv[db][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-  float dsum = 0.f;
+  double dsum = 0.0;  // sum of ds; per-tile fp32 partials are added in fp64
 
   const int nqt = (N + BMQ - 1) / BMQ;
   const int qt0 = CAUSAL ? kv0 / BMQ : 0;
@@ -578,6 +595,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     }
     const bool diag = CAUSAL && (m0 < kw0 + KPW - 1);
     const bool edge = m0 + BMQ > N || kw0 + KPW > N;
+    float tsum = 0.f;
 #pragma unroll
     for (int qb = 0; qb < 4; ++qb) {
 #pragma unroll
@@ -603,10 +621,11 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
           float ds = rcoef * u9 * (dw[qb][kb][i] - rD);
           if (u == rM && u > 0.f) ds += rG;
           dw[qb][kb][i] = ds;
-          dsum += ds;
+          tsum += ds;
         }
       }
     }
+    dsum += (double)tsum;
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
       bf16x8 wf[KB], sf[KB];
@@ -651,16 +670,16 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
       }
     }
   }
-  dsum = wave_sum(dsum);
+  dsum = wave_sum_d(dsum);
   if (lane == 0) p.partials[((int64_t)bh * p.nkvb + kvb) * 4 + w] = dsum;
 }
 
 // dtau = -(sum of all ds partials) / scale, summed in fp64 by one block in a fixed order.
-__global__ __launch_bounds__(256) void flash_dtau_kernel(const float* partials, int64_t n,
+__global__ __launch_bounds__(256) void flash_dtau_kernel(const double* partials, int64_t n,
                                                          float scale, float* dtau) {
   __shared__ double red[256];
   double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < n; i += 256) acc += (double)partials[i];
+  for (int64_t i = threadIdx.x; i < n; i += 256) acc += partials[i];
   red[threadIdx.x] = acc;
   __syncthreads();
   for (int s = 128; s > 0; s >>= 1) {
@@ -685,36 +704,42 @@ int launch_fwd_d(const FwdParams& fp, bool causal, bool has_gamma, hipStream_t s
 }
 
 template <int D>
-int launch_bwd_d(const BwdParams& bp, bool causal, bool has_gamma, hipStream_t st) {
-  const int64_t rows = (int64_t)bp.B * bp.H * bp.N;
-  const int rpb = 256 / (D / 8);
-  const dim3 gpre((unsigned)((rows + rpb - 1) / rpb)), block(256);
-  if (has_gamma) hipLaunchKernelGGL((flash_bwd_pre_kernel<D, true>), gpre, block, 0, st, bp);
-  else hipLaunchKernelGGL((flash_bwd_pre_kernel<D, false>), gpre, block, 0, st, bp);
-  int rc = launch_status("pnfx_flash_bwd(pre)");
-  if (rc) return rc;
-  const int nqb = (bp.N + 127) / 128;
-  const dim3 gdq((unsigned)(nqb * bp.B * bp.H));
-  const dim3 gkv((unsigned)(bp.nkvb * bp.B * bp.H));
-  if (causal) {
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, true>), gkv, block, 0, st, bp);
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true>), gdq, block, 0, st, bp);
-  } else {
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, false>), gkv, block, 0, st, bp);
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false>), gdq, block, 0, st, bp);
+int launch_bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, hipStream_t st) {
+  const dim3 block(256);
+  if (stages & PNFX_BWD_PREPARE) {
+    const int64_t rows = (int64_t)bp.B * bp.H * bp.N;
+    const int rpb = 256 / (D / 8);
+    const dim3 gpre((unsigned)((rows + rpb - 1) / rpb));
+    if (has_gamma) hipLaunchKernelGGL((flash_bwd_pre_kernel<D, true>), gpre, block, 0, st, bp);
+    else hipLaunchKernelGGL((flash_bwd_pre_kernel<D, false>), gpre, block, 0, st, bp);
+    const int rc = launch_status("pnfx_flash_bwd(prepare)");
+    if (rc) return rc;
   }
-  rc = launch_status("pnfx_flash_bwd(main)");
-  if (rc) return rc;
-  hipLaunchKernelGGL(flash_dtau_kernel, dim3(1), block, 0, st, bp.partials,
-                     (int64_t)bp.B * bp.H * bp.nkvb * 4, bp.scale, bp.dtau);
-  return launch_status("pnfx_flash_bwd(dtau)");
+  if (stages & PNFX_BWD_DKDV) {
+    const dim3 gkv((unsigned)(bp.nkvb * bp.B * bp.H));
+    if (causal) hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, true>), gkv, block, 0, st, bp);
+    else hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, false>), gkv, block, 0, st, bp);
+    hipLaunchKernelGGL(flash_dtau_kernel, dim3(1), block, 0, st, bp.partials,
+                       (int64_t)bp.B * bp.H * bp.nkvb * 4, bp.scale, bp.dtau);
+    const int rc = launch_status("pnfx_flash_bwd(dkdv)");
+    if (rc) return rc;
+  }
+  if (stages & PNFX_BWD_DQ) {
+    const int nqb = (bp.N + 127) / 128;
+    const dim3 gdq((unsigned)(nqb * bp.B * bp.H));
+    if (causal) hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true>), gdq, block, 0, st, bp);
+    else hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false>), gdq, block, 0, st, bp);
+    const int rc = launch_status("pnfx_flash_bwd(dq)");
+    if (rc) return rc;
+  }
+  return PNFX_OK;
 }
 
 }  // namespace
 
 int64_t bwd_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D) {
   const int64_t rc = B * H * N * 8 * 4;
-  const int64_t parts = B * H * bwd_nkvb(N, D) * 4 * 4;
+  const int64_t parts = B * H * bwd_nkvb(N, D) * 4 * 8;
   return ((rc + 255) / 256) * 256 + ((parts + 255) / 256) * 256;
 }
 
@@ -729,12 +754,13 @@ int flash_fwd_bf16(const FwdParams& fp, int64_t D, bool causal, bool has_gamma, 
   return PNFX_EUNSUPPORTED;
 }
 
-int flash_bwd_bf16(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, hipStream_t st) {
+int flash_bwd_bf16(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, int stages,
+                   hipStream_t st) {
   switch (D) {
-    case 16: return launch_bwd_d<16>(bp, causal, has_gamma, st);
-    case 32: return launch_bwd_d<32>(bp, causal, has_gamma, st);
-    case 64: return launch_bwd_d<64>(bp, causal, has_gamma, st);
-    case 128: return launch_bwd_d<128>(bp, causal, has_gamma, st);
+    case 16: return launch_bwd_d<16>(bp, causal, has_gamma, stages, st);
+    case 32: return launch_bwd_d<32>(bp, causal, has_gamma, stages, st);
+    case 64: return launch_bwd_d<64>(bp, causal, has_gamma, stages, st);
+    case 128: return launch_bwd_d<128>(bp, causal, has_gamma, stages, st);
   }
   set_error("flash: head dim %lld not in {16, 32, 64, 128}", (long long)D);
   return PNFX_EUNSUPPORTED;

@@ -202,7 +202,7 @@ __global__ __launch_bounds__(64) void f32_bwd_dkdv_kernel(BwdParams p) {
     dk[d] = 0.f;
     dv[d] = 0.f;
   }
-  float dsum = 0.f;
+  double dsum = 0.0;
   const int nqt = (N + TB - 1) / TB;
   const int qt0 = CAUSAL ? blockIdx.x : 0;
   for (int qt = qt0; qt < nqt; ++qt) {
@@ -223,6 +223,7 @@ __global__ __launch_bounds__(64) void f32_bwd_dkdv_kernel(BwdParams p) {
     }
     if (!has) continue;
     const int imax = min(TB, N - m0);
+    float tsum = 0.f;
     for (int i = 0; i < imax; ++i) {
       if (CAUSAL && m0 + i < key) continue;
       float s = 0.f, dw = 0.f;
@@ -237,15 +238,16 @@ __global__ __launch_bounds__(64) void f32_bwd_dkdv_kernel(BwdParams p) {
       const float w = u8 * u2 * RC[i][1];
       float ds = RC[i][2] * (u8 * u) * (dw - RC[i][3]);
       if (u == RC[i][0] && u > 0.f) ds += RC[i][4];
-      dsum += ds;
+      tsum += ds;
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         dv[d] = __builtin_fmaf(w, dOs[i][d], dv[d]);
         dk[d] = __builtin_fmaf(ds, Qs[i][d], dk[d]);
       }
     }
+    dsum += (double)tsum;
   }
-  dsum = wave_sum(dsum);
+  dsum = wave_sum_d(dsum);
   if (lane == 0) p.partials[(int64_t)bh * gridDim.x + blockIdx.x] = dsum;
   if (!has) return;
   float* dK = static_cast<float*>(p.dk) + b * p.dksb + h * p.dksh + (int64_t)key * p.dksn;
@@ -257,11 +259,11 @@ __global__ __launch_bounds__(64) void f32_bwd_dkdv_kernel(BwdParams p) {
   }
 }
 
-__global__ __launch_bounds__(256) void f32_dtau_kernel(const float* partials, int64_t n, float scale,
+__global__ __launch_bounds__(256) void f32_dtau_kernel(const double* partials, int64_t n, float scale,
                                                        float* dtau) {
   __shared__ double red[256];
   double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < n; i += 256) acc += (double)partials[i];
+  for (int64_t i = threadIdx.x; i < n; i += 256) acc += partials[i];
   red[threadIdx.x] = acc;
   __syncthreads();
   for (int s = 128; s > 0; s >>= 1) {
@@ -285,27 +287,32 @@ int fwd_d(const FwdParams& fp, bool causal, bool has_gamma, hipStream_t st) {
 }
 
 template <int D>
-int bwd_d(const BwdParams& bp, bool causal, bool has_gamma, hipStream_t st) {
-  const int64_t rows = (int64_t)bp.B * bp.H * bp.N;
-  const dim3 gpre((unsigned)((rows + 255) / 256));
-  if (has_gamma) hipLaunchKernelGGL((f32_bwd_pre_kernel<D, true>), gpre, dim3(256), 0, st, bp);
-  else hipLaunchKernelGGL((f32_bwd_pre_kernel<D, false>), gpre, dim3(256), 0, st, bp);
-  int rc = launch_status("pnfx_flash_bwd(f32 pre)");
-  if (rc) return rc;
+int bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, hipStream_t st) {
   const unsigned nb = (unsigned)((bp.N + TB - 1) / TB);
   const dim3 grid(nb, (unsigned)(bp.B * bp.H)), block(TB);
-  if (causal) {
-    hipLaunchKernelGGL((f32_bwd_dkdv_kernel<D, true>), grid, block, 0, st, bp);
-    hipLaunchKernelGGL((f32_bwd_dq_kernel<D, true>), grid, block, 0, st, bp);
-  } else {
-    hipLaunchKernelGGL((f32_bwd_dkdv_kernel<D, false>), grid, block, 0, st, bp);
-    hipLaunchKernelGGL((f32_bwd_dq_kernel<D, false>), grid, block, 0, st, bp);
+  if (stages & PNFX_BWD_PREPARE) {
+    const int64_t rows = (int64_t)bp.B * bp.H * bp.N;
+    const dim3 gpre((unsigned)((rows + 255) / 256));
+    if (has_gamma) hipLaunchKernelGGL((f32_bwd_pre_kernel<D, true>), gpre, dim3(256), 0, st, bp);
+    else hipLaunchKernelGGL((f32_bwd_pre_kernel<D, false>), gpre, dim3(256), 0, st, bp);
+    const int rc = launch_status("pnfx_flash_bwd(f32 prepare)");
+    if (rc) return rc;
   }
-  rc = launch_status("pnfx_flash_bwd(f32 main)");
-  if (rc) return rc;
-  hipLaunchKernelGGL(f32_dtau_kernel, dim3(1), dim3(256), 0, st, bp.partials,
-                     (int64_t)bp.B * bp.H * nb, bp.scale, bp.dtau);
-  return launch_status("pnfx_flash_bwd(f32 dtau)");
+  if (stages & PNFX_BWD_DKDV) {
+    if (causal) hipLaunchKernelGGL((f32_bwd_dkdv_kernel<D, true>), grid, block, 0, st, bp);
+    else hipLaunchKernelGGL((f32_bwd_dkdv_kernel<D, false>), grid, block, 0, st, bp);
+    hipLaunchKernelGGL(f32_dtau_kernel, dim3(1), dim3(256), 0, st, bp.partials,
+                       (int64_t)bp.B * bp.H * nb, bp.scale, bp.dtau);
+    const int rc = launch_status("pnfx_flash_bwd(f32 dkdv)");
+    if (rc) return rc;
+  }
+  if (stages & PNFX_BWD_DQ) {
+    if (causal) hipLaunchKernelGGL((f32_bwd_dq_kernel<D, true>), grid, block, 0, st, bp);
+    else hipLaunchKernelGGL((f32_bwd_dq_kernel<D, false>), grid, block, 0, st, bp);
+    const int rc = launch_status("pnfx_flash_bwd(f32 dq)");
+    if (rc) return rc;
+  }
+  return PNFX_OK;
 }
 
 }  // namespace
@@ -321,12 +328,13 @@ int flash_fwd_f32(const FwdParams& fp, int64_t D, bool causal, bool has_gamma, h
   return PNFX_EUNSUPPORTED;
 }
 
-int flash_bwd_f32(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, hipStream_t st) {
+int flash_bwd_f32(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, int stages,
+                  hipStream_t st) {
   switch (D) {
-    case 16: return bwd_d<16>(bp, causal, has_gamma, st);
-    case 32: return bwd_d<32>(bp, causal, has_gamma, st);
-    case 64: return bwd_d<64>(bp, causal, has_gamma, st);
-    case 128: return bwd_d<128>(bp, causal, has_gamma, st);
+    case 16: return bwd_d<16>(bp, causal, has_gamma, stages, st);
+    case 32: return bwd_d<32>(bp, causal, has_gamma, stages, st);
+    case 64: return bwd_d<64>(bp, causal, has_gamma, stages, st);
+    case 128: return bwd_d<128>(bp, causal, has_gamma, stages, st);
   }
   set_error("flash(f32): head dim %lld not in {16, 32, 64, 128}", (long long)D);
   return PNFX_EUNSUPPORTED;

@@ -86,9 +86,9 @@ def _flash_attention(q, k, v, score_tau, scale, gamma, causal_mask, o_bnhd=False
     if not q.is_cuda:
         raise RuntimeError("flash_pn_fir_tau_attention runs on the GPU only (as in the reference)")
     has_gamma = gamma is not None and gamma > 0.0
-    o, _, _, _, _ = torch.ops.pnfx.flash_fwd(q, k, v, score_tau, float(scale),
-                                             float(gamma) if has_gamma else 0.0, has_gamma,
-                                             bool(causal_mask), bool(o_bnhd))
+    o = torch.ops.pnfx.flash_fwd(q, k, v, score_tau, float(scale),
+                                 float(gamma) if has_gamma else 0.0, has_gamma,
+                                 bool(causal_mask), bool(o_bnhd))[0]
     return o
 
 
@@ -118,9 +118,10 @@ def flash_pn_fir_tau_attention_with_stats(q, k_tilde, v, score_tau, scale=None, 
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     has_gamma = gamma is not None and gamma > 0.0
-    return torch.ops.pnfx.flash_fwd(q, k_tilde, v, score_tau, float(scale),
-                                    float(gamma) if has_gamma else 0.0, has_gamma,
-                                    bool(causal_mask), False)
+    o, _, M, Z, Nm, mask = torch.ops.pnfx.flash_fwd(q, k_tilde, v, score_tau, float(scale),
+                                                   float(gamma) if has_gamma else 0.0, has_gamma,
+                                                   bool(causal_mask), False)
+    return o, M, Z, Nm, mask
 
 
 def tile_mask_64(mask32: torch.Tensor) -> torch.Tensor:

@@ -178,62 +178,72 @@ def _bhnd(t: Tensor, name: str, bf16: bool) -> Tensor:
     return t if ok else t.contiguous()
 
 
+def _ptr4(t: Tensor) -> tuple[int, int, int, int]:
+    """(data pointer, batch, head, row strides) of a [B,H,N,D] operand for the C ABI."""
+    return t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)
+
+
+def _new_o(q: Tensor, o_bnhd: bool) -> Tensor:
+    B, H, N, D = q.shape
+    if o_bnhd:
+        return torch.empty((B, N, H, D), device=q.device, dtype=q.dtype).permute(0, 2, 1, 3)
+    return torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
+
+
 @torch.library.custom_op("pnfx::flash_fwd", mutates_args=(), device_types="cuda")
 def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma: float,
               has_gamma: bool, causal: bool,
-              o_bnhd: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Flash forward on [B,H,N,D]; returns (O, M, Z, Nmax, tile_mask).
+              o_bnhd: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Flash forward on [B,H,N,D]; returns (O, O_lo, M, Z, Nmax, tile_mask).
 
     O has shape [B,H,N,D]; with o_bnhd it is backed by a [B,N,H,D] buffer so that
-    the caller's transpose back to [B,N,H*D] is free.  tile_mask is uint8
-    [B*H, ceil(N/32), ceil(N/64)] (32-query x 64-key sub-tile activity).
+    the caller's transpose back to [B,N,H*D] is free.  O_lo (bf16 only; empty for
+    fp32) is O's bf16 rounding residual, saved for an accurate backward.
+    tile_mask is uint8 [B*H, ceil(N/32), ceil(N/64)] (32-query x 64-key sub-tile
+    activity).
     """
     B, H, N, D = q.shape
     code = _code(q, "flash")
     bf = code == _lib.PNFX_BF16
     q, k, v = _bhnd(q, "q", bf), _bhnd(k, "k", bf), _bhnd(v, "v", bf)
-    if o_bnhd:
-        o = torch.empty((B, N, H, D), device=q.device, dtype=q.dtype).permute(0, 2, 1, 3)
-    else:
-        o = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
+    o = _new_o(q, o_bnhd)
+    o_lo = _new_o(q, o_bnhd) if bf else q.new_empty(0)
     M = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     Z = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     Nm = torch.empty((B, H, N), device=q.device, dtype=torch.int32)
     mask = torch.empty((B * H, (N + 31) // 32, (N + 63) // 64), device=q.device, dtype=torch.uint8)
     t32 = _tau32(tau)
     rc = _lib.lib().pnfx_flash_fwd(
-        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
-        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
-        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
-        o.data_ptr(), o.stride(0), o.stride(1), o.stride(2),
+        *_ptr4(q), *_ptr4(k), *_ptr4(v), *_ptr4(o), o_lo.data_ptr() if bf else None,
         M.data_ptr(), Z.data_ptr(), Nm.data_ptr(), mask.data_ptr(), B, H, N, D,
         t32.data_ptr(), scale, gamma, int(has_gamma), int(causal), code, _stream(q))
     _lib.check(rc, "pnfx_flash_fwd")
-    return o, M, Z, Nm, mask
+    return o, o_lo, M, Z, Nm, mask
 
 
 @flash_fwd.register_fake
 def _(q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd):
     B, H, N, D = q.shape
-    if o_bnhd:
-        o = q.new_empty((B, N, H, D)).permute(0, 2, 1, 3)
-    else:
-        o = q.new_empty((B, H, N, D))
+    o = _new_o(q, o_bnhd)
+    o_lo = _new_o(q, o_bnhd) if q.dtype == torch.bfloat16 else q.new_empty(0)
     f = lambda dt: q.new_empty((B, H, N), dtype=dt)  # noqa: E731
     mask = q.new_empty((B * H, (N + 31) // 32, (N + 63) // 64), dtype=torch.uint8)
-    return o, f(torch.float32), f(torch.float32), f(torch.int32), mask
+    return o, o_lo, f(torch.float32), f(torch.float32), f(torch.int32), mask
 
 
 @torch.library.custom_op("pnfx::flash_bwd", mutates_args=(), device_types="cuda")
-def flash_bwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, o: Tensor, do: Tensor, M: Tensor,
-              Z: Tensor, Nmax: Tensor, mask: Tensor, scale: float, gamma: float, has_gamma: bool,
-              causal: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+def flash_bwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, o: Tensor, o_lo: Tensor, do: Tensor,
+              M: Tensor, Z: Tensor, Nmax: Tensor, mask: Tensor, scale: float, gamma: float,
+              has_gamma: bool, causal: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Deterministic flash backward; returns (dq, dk, dv, dtau) with dtau a 1-element fp32 tensor."""
     B, H, N, D = q.shape
     code = _code(q, "flash")
     bf = code == _lib.PNFX_BF16
     q, k, v = _bhnd(q, "q", bf), _bhnd(k, "k", bf), _bhnd(v, "v", bf)
+    use_lo = bf and o_lo.numel() == o.numel() and o_lo.stride() == o.stride()
     o = _bhnd(o, "o", bf)
+    if use_lo and o_lo.stride() != o.stride():
+        use_lo = False
     do = _bhnd(do.to(q.dtype), "dO", bf)
     dq = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
     dk = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
@@ -244,23 +254,16 @@ def flash_bwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, o: Tensor, do: Tenso
     ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
     t32 = _tau32(tau)
     rc = L.pnfx_flash_bwd(
-        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
-        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
-        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
-        o.data_ptr(), o.stride(0), o.stride(1), o.stride(2),
-        do.data_ptr(), do.stride(0), do.stride(1), do.stride(2),
-        M.data_ptr(), Z.data_ptr(), Nmax.data_ptr(), mask.data_ptr(),
-        dq.data_ptr(), dq.stride(0), dq.stride(1), dq.stride(2),
-        dk.data_ptr(), dk.stride(0), dk.stride(1), dk.stride(2),
-        dv.data_ptr(), dv.stride(0), dv.stride(1), dv.stride(2),
-        dtau.data_ptr(), ws.data_ptr(), ws_bytes, B, H, N, D,
+        *_ptr4(q), *_ptr4(k), *_ptr4(v), *_ptr4(o), o_lo.data_ptr() if use_lo else None,
+        *_ptr4(do), M.data_ptr(), Z.data_ptr(), Nmax.data_ptr(), mask.data_ptr(),
+        *_ptr4(dq), *_ptr4(dk), *_ptr4(dv), dtau.data_ptr(), ws.data_ptr(), ws_bytes, B, H, N, D,
         t32.data_ptr(), scale, gamma, int(has_gamma), int(causal), code, _stream(q))
     _lib.check(rc, "pnfx_flash_bwd")
     return dq, dk, dv, dtau
 
 
 @flash_bwd.register_fake
-def _(q, k, v, tau, o, do, M, Z, Nmax, mask, scale, gamma, has_gamma, causal):
+def _(q, k, v, tau, o, o_lo, do, M, Z, Nmax, mask, scale, gamma, has_gamma, causal):
     return (torch.empty_like(q, memory_format=torch.contiguous_format),
             torch.empty_like(k, memory_format=torch.contiguous_format),
             torch.empty_like(v, memory_format=torch.contiguous_format),
@@ -269,14 +272,14 @@ def _(q, k, v, tau, o, do, M, Z, Nmax, mask, scale, gamma, has_gamma, causal):
 
 def _flash_setup(ctx, inputs, output):
     q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd = inputs
-    o, M, Z, Nm, mask = output
-    ctx.save_for_backward(q, k, v, tau, o, M, Z, Nm, mask)
+    o, o_lo, M, Z, Nm, mask = output
+    ctx.save_for_backward(q, k, v, tau, o, o_lo, M, Z, Nm, mask)
     ctx.args = (scale, gamma, has_gamma, causal)
 
 
-def _flash_backward(ctx, do, dM, dZ, dN, dmask):
-    q, k, v, tau, o, M, Z, Nm, mask = ctx.saved_tensors
-    dq, dk, dv, dt = flash_bwd(q, k, v, tau, o, do, M, Z, Nm, mask, *ctx.args)
+def _flash_backward(ctx, do, do_lo, dM, dZ, dN, dmask):
+    q, k, v, tau, o, o_lo, M, Z, Nm, mask = ctx.saved_tensors
+    dq, dk, dv, dt = flash_bwd(q, k, v, tau, o, o_lo, do, M, Z, Nm, mask, *ctx.args)
     return dq, dk, dv, dt.to(tau.dtype).view_as(tau), None, None, None, None, None
 
 

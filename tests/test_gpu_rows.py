@@ -49,6 +49,5 @@ def test_rows_stats_and_silent_rows(dev):
     assert torch.all(w[0, 0, 10] == 0)
     np.testing.assert_allclose(M.cpu().numpy(), Mo.reshape(-1), rtol=1e-6)
     np.testing.assert_allclose(Z.cpu().numpy(), Zo.reshape(-1), rtol=1e-5)
-    # row sums equal the gate
-    g = Mo / (Mo + 0.5)
-    np.testing.assert_allclose(w.sum(-1).cpu().numpy().reshape(-1), g.reshape(-1), rtol=1e-5, atol=1e-7)
+    # row sums equal gate * mass / (mass + 1e-12), i.e. the gate unless the mass is tiny
+    np.testing.assert_allclose(w.sum(-1).cpu().numpy().reshape(-1), Wo.sum(-1).reshape(-1), rtol=1e-5, atol=1e-7)
