@@ -38,38 +38,69 @@ __device__ __forceinline__ int perm_row(int blk, int r) {
 
 __device__ __forceinline__ bf16x8 ld16(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
-// Stage rows [row0, row0 + ROWS) of a [N, D] slice (row stride sn) into LDS, row-major with
-// row stride STR and zero padding up to DK columns and beyond N.
-template <int ROWS, int D, int DK, int STR>
-__device__ __forceinline__ void stage_rows(bf16* dst, const bf16* src, int64_t sn, int row0, int N,
-                                           int tid) {
-#pragma unroll
-  for (int c = tid; c < ROWS * (DK / 8); c += 256) {
-    const int row = c / (DK / 8), col = (c % (DK / 8)) * 8;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (row0 + row < N && col < D)
-      v = *reinterpret_cast<const u32x4*>(src + (int64_t)(row0 + row) * sn + col);
-    *reinterpret_cast<u32x4*>(dst + row * STR + col) = v;
-  }
-}
+// Register-staged copy of rows [row0, row0 + ROWS) of an [N, D] bf16 slice (row stride sn).
+// Chunk c of a thread covers rows 2*(c / CPR) and 2*(c / CPR) + 1 at columns
+// 8*(c % CPR) .. +7 (CPR = D/8 chunks per row), so a wave's load instruction reads whole
+// contiguous rows.  load() issues the global reads into registers (rows >= N read as zero);
+// store_rows() writes them row-major (row stride STR) and store_cols() transposed
+// (dst[col * STR + row]) -- one global read serves both LDS layouts.
+template <int ROWS, int D>
+struct PairTile {
+  static constexpr int CPR = D / 8;
+  static constexpr int NCH = (ROWS / 2) * CPR;
+  static constexpr int PER = (NCH + 255) / 256;
+  u32x4 a[PER], b[PER];
 
-// Stage rows [row0, row0 + ROWS) transposed: dst[d * STR + row] (D rows of ROWS columns).
-template <int ROWS, int D, int STR>
-__device__ __forceinline__ void stage_rows_t(bf16* dst, const bf16* src, int64_t sn, int row0,
-                                             int N, int tid) {
+  __device__ __forceinline__ void load(const bf16* src, int64_t sn, int row0, int N, int tid) {
 #pragma unroll
-  for (int c = tid; c < (ROWS / 2) * (D / 8); c += 256) {
-    const int rp = c % (ROWS / 2), col = (c / (ROWS / 2)) * 8;
-    const int row = 2 * rp;
-    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
-    if (row0 + row < N) a = *reinterpret_cast<const u32x4*>(src + (int64_t)(row0 + row) * sn + col);
-    if (row0 + row + 1 < N)
-      b = *reinterpret_cast<const u32x4*>(src + (int64_t)(row0 + row + 1) * sn + col);
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + 256 * i;
+      a[i] = u32x4{0u, 0u, 0u, 0u};
+      b[i] = u32x4{0u, 0u, 0u, 0u};
+      if (NCH % 256 == 0 || c < NCH) {
+        const int r = row0 + 2 * (c / CPR), col = 8 * (c % CPR);
+        if (r < N) a[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)r * sn + col);
+        if (r + 1 < N) b[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(r + 1) * sn + col);
+      }
+    }
+  }
+  template <int STR>
+  __device__ __forceinline__ void store_rows(bf16* dst, int tid) const {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t lo = (e & 1) ? (a[e >> 1] >> 16) : (a[e >> 1] & 0xffffu);
-      const uint32_t hi = (e & 1) ? (b[e >> 1] & 0xffff0000u) : (b[e >> 1] << 16);
-      *reinterpret_cast<uint32_t*>(dst + (col + e) * STR + row) = lo | hi;
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + 256 * i;
+      if (NCH % 256 == 0 || c < NCH) {
+        const int r = 2 * (c / CPR), col = 8 * (c % CPR);
+        *reinterpret_cast<u32x4*>(dst + r * STR + col) = a[i];
+        *reinterpret_cast<u32x4*>(dst + (r + 1) * STR + col) = b[i];
+      }
+    }
+  }
+  template <int STR>
+  __device__ __forceinline__ void store_cols(bf16* dst, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + 256 * i;
+      if (NCH % 256 == 0 || c < NCH) {
+        const int r = 2 * (c / CPR), col = 8 * (c % CPR);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t lo = (e & 1) ? (a[i][e >> 1] >> 16) : (a[i][e >> 1] & 0xffffu);
+          const uint32_t hi = (e & 1) ? (b[i][e >> 1] & 0xffff0000u) : (b[i][e >> 1] << 16);
+          *reinterpret_cast<uint32_t*>(dst + (col + e) * STR + r) = lo | hi;
+        }
+      }
+    }
+  }
+};
+
+// Zero columns [D, DK) of a row-major LDS tile (the k-padding of the 32-wide MFMA when D < 32).
+template <int ROWS, int D, int DK, int STR>
+__device__ __forceinline__ void zero_pad_cols(bf16* dst, int tid) {
+  if (D < DK) {
+    for (int c = tid; c < ROWS * ((DK - D) / 8); c += 256) {
+      const int r = c / ((DK - D) / 8), col = D + 8 * (c % ((DK - D) / 8));
+      *reinterpret_cast<u32x4*>(dst + r * STR + col) = u32x4{0u, 0u, 0u, 0u};
     }
   }
 }
@@ -94,6 +125,33 @@ __device__ __forceinline__ void map_block(int nblk, int BH, bool heavy_last_inde
 }
 
 // ------------------------------------------------------------------------------ forward
+// s -> u = relu(fma(s, scale, -tau)) in place for the 16 scores a lane holds in one 32-key
+// half tile (S^T layout: key blocks 2*hf, 2*hf+1 x 2 query blocks x 4), zeroing keys past
+// the causal diagonal or N when MASK; returns the lane's per-query-row maximum in tm.
+template <bool MASK>
+__device__ __forceinline__ void rectify_kq(f32x4 (&s)[2][2], float (&tm)[2], float scale, float ntau,
+                                           int n0, int hf, int qrow0, int N, bool causal, int g,
+                                           int r16) {
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    float mx = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float u = fmaxf(__builtin_fmaf(s[kk][qb][i], scale, ntau), 0.f);
+        if (MASK) {
+          const int key = n0 + perm_row(2 * hf + kk, 4 * g + i);
+          const int qrow = qrow0 + 16 * qb + r16;
+          if ((causal && key > qrow) || key >= N) u = 0.f;
+        }
+        s[kk][qb][i] = u;
+        mx = fmaxf(mx, u);
+      }
+    tm[qb] = mx;
+  }
+}
+
 template <int D, bool CAUSAL, bool HAS_GAMMA>
 __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
   constexpr int BM = 128, BN = 64;
@@ -102,8 +160,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
   constexpr int DB = D / 16;
   constexpr int KSTR = DK + 8;
   constexpr int VSTR = BN + 8;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[BN * KSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Vt[D * VSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Ks[2][BN * KSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Vt[2][D * VSTR];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
   const int N = p.N;
@@ -154,91 +212,87 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
   uint8_t* mrow =
       (p.mask && has_rows) ? p.mask + ((int64_t)bh * p.nq32 + (qrow0 >> 5)) * p.nk64 : nullptr;
 
+  // Software pipeline: tile t+1 is read from HBM/L2 into registers while tile t is
+  // computed from LDS, then committed to the other LDS buffer; one barrier per tile.
+  PairTile<BN, D> kt, vt;
+  zero_pad_cols<BN, D, DK, KSTR>(Ks[0], tid);
+  zero_pad_cols<BN, D, DK, KSTR>(Ks[1], tid);
+  kt.load(K, p.ksn, 0, N, tid);
+  vt.load(V, p.vsn, 0, N, tid);
+  kt.template store_rows<KSTR>(Ks[0], tid);
+  vt.template store_cols<VSTR>(Vt[0], tid);
+
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = t * BN;
+    const int cur = t & 1;
     __syncthreads();
-    stage_rows<BN, D, DK, KSTR>(Ks, K, p.ksn, n0, N, tid);
-    stage_rows_t<BN, D, VSTR>(Vt, V, p.vsn, n0, N, tid);
-    __syncthreads();
-
+    const bool pre = t + 1 < ntiles;
+    if (pre) {
+      kt.load(K, p.ksn, n0 + BN, N, tid);
+      vt.load(V, p.vsn, n0 + BN, N, tid);
+    }
     bool active = false;
     if (has_rows && !(CAUSAL && n0 > qrow0 + 31)) {
-      f32x4 s[4][2];
+      const bf16* Kc = Ks[cur];
+      const bf16* Vc = Vt[cur];
+      const bool masked = (CAUSAL && n0 + BN - 1 > qrow0) || n0 + BN > N;
+      // Two 32-key halves: each half's scores are exactly one k-step of the P.V MFMA.
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const bf16* kr = Ks + perm_row(kb, r16) * KSTR + 8 * g;
-        bf16x8 kf[KS];
+      for (int hf = 0; hf < 2; ++hf) {
+        if (CAUSAL && n0 + 32 * hf > qrow0 + 31) break;  // half entirely above the diagonal
+        f32x4 s[2][2];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) kf[ks] = ld16(kr + 32 * ks);
+        for (int kk = 0; kk < 2; ++kk) {
+          const bf16* kr = Kc + perm_row(2 * hf + kk, r16) * KSTR + 8 * g;
+          bf16x8 kf[KS];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          f32x4 a = {0.f, 0.f, 0.f, 0.f};
+          for (int ks = 0; ks < KS; ++ks) kf[ks] = ld16(kr + 32 * ks);
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(kf[ks], qf[qb][ks], a);
-          s[kb][qb] = a;
-        }
-      }
-      const bool diag = CAUSAL && (n0 + BN - 1 > qrow0);
-      const bool edge = n0 + BN > N;
-      bool any = false;
+          for (int qb = 0; qb < 2; ++qb) {
+            f32x4 a4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float sv = __builtin_fmaf(s[kb][qb][i], scale, ntau);
-            float u = sv > 0.f ? sv : 0.f;
-            if (diag || edge) {
-              const int key = n0 + perm_row(kb, 4 * g + i);
-              const int qrow = qrow0 + 16 * qb + r16;
-              if ((CAUSAL && key > qrow) || key >= N) u = 0.f;
-            }
-            s[kb][qb][i] = u;
-            any |= u > 0.f;
+            for (int ks = 0; ks < KS; ++ks) a4 = mfma16x16x32(kf[ks], qf[qb][ks], a4);
+            s[kk][qb] = a4;
           }
-      active = __any(any);
-      if (active) {
+        }
+        float tm[2];
+        if (masked)
+          rectify_kq<true>(s, tm, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+        else
+          rectify_kq<false>(s, tm, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+        if (!__any(fmaxf(tm[0], tm[1]) > 0.f)) continue;  // silent half: skip P and P.V
+        active = true;
+        bf16x8 pf[2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
-          float tm = 0.f;
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) tm = fmaxf(tm, s[kb][qb][i]);
-          const float mnew = fmaxf(mrun[qb], tm);
+          const float mnew = fmaxf(mrun[qb], tm[qb]);
           int c = (mnew == mrun[qb]) ? cnt[qb] : 0;
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
+          for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) c += (s[kb][qb][i] == mnew) ? 1 : 0;
+            for (int i = 0; i < 4; ++i) c += (s[kk][qb][i] == mnew) ? 1 : 0;
           cnt[qb] = c;
           mrun[qb] = mnew;
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s[kb][qb][i] = pow10f_(s[kb][qb][i]);
+          pf[qb] = pack8(pow10f_(s[0][qb][0]), pow10f_(s[0][qb][1]), pow10f_(s[0][qb][2]),
+                         pow10f_(s[0][qb][3]), pow10f_(s[1][qb][0]), pow10f_(s[1][qb][1]),
+                         pow10f_(s[1][qb][2]), pow10f_(s[1][qb][3]));
         }
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp) {
-          bf16x8 pf[2];
+        for (int db = 0; db < DB; ++db) {
+          const bf16x8 vf = ld16(Vc + (16 * db + r16) * VSTR + 32 * hf + 8 * g);
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
-            pf[qb] = pack8(s[2 * tp][qb][0], s[2 * tp][qb][1], s[2 * tp][qb][2], s[2 * tp][qb][3],
-                           s[2 * tp + 1][qb][0], s[2 * tp + 1][qb][1], s[2 * tp + 1][qb][2],
-                           s[2 * tp + 1][qb][3]);
-#pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            const bf16x8 vf = ld16(Vt + (16 * db + r16) * VSTR + 32 * tp + 8 * g);
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(vf, pf[qb], acc[db][qb]);
-          }
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) accm[qb] = mfma16x16x32(ones, pf[qb], accm[qb]);
+          for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(vf, pf[qb], acc[db][qb]);
         }
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) accm[qb] = mfma16x16x32(ones, pf[qb], accm[qb]);
       }
+      active = __any(active);
     }
     if (mrow && lane == 0) mrow[t] = active ? 1 : 0;
+    if (pre) {
+      kt.template store_rows<KSTR>(Ks[cur ^ 1], tid);
+      vt.template store_cols<VSTR>(Vt[cur ^ 1], tid);
+    }
   }
   if (mrow && lane == 0)
     for (int t = ntiles; t < p.nk64; ++t) mrow[t] = 0;
@@ -333,7 +387,35 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   }
 }
 
-// dQ: query-parallel, same tiling as the forward (4 waves x 32 rows, 64-key tiles).
+// ds = (c u^9)(dW - D) + [u == M] G for the 16 scores of a lane in one 32-key half tile
+// (S^T layout, query row per lane), written over s.  Row constants are the lane's two rows.
+template <bool MASK>
+__device__ __forceinline__ void ds_kq(f32x4 (&s)[2][2], const f32x4 (&dw)[2][2], const float (&rM)[2],
+                                      const float (&rc)[2], const float (&rD)[2], const float (&rG)[2],
+                                      float scale, float ntau, int n0, int hf, int qrow0, int N,
+                                      bool causal, int g, int r16) {
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float u = fmaxf(__builtin_fmaf(s[kk][qb][i], scale, ntau), 0.f);
+        if (MASK) {
+          const int key = n0 + perm_row(2 * hf + kk, 4 * g + i);
+          const int qrow = qrow0 + 16 * qb + r16;
+          if ((causal && key > qrow) || key >= N) u = 0.f;
+        }
+        const float u2 = u * u;
+        const float u4 = u2 * u2;
+        const float u9 = u4 * u4 * u;
+        const float tie = (u == rM[qb]) ? rG[qb] : 0.f;  // G = 0 on silent rows
+        s[kk][qb][i] = __builtin_fmaf(rc[qb] * u9, dw[kk][qb][i] - rD[qb], tie);
+      }
+}
+
+// dQ: query-parallel, same tiling as the forward (4 waves x 32 rows, 64-key tiles), K and V
+// tiles software-pipelined through LDS (double-buffered when it fits).
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   constexpr int BM = 128, BN = 64;
@@ -342,9 +424,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   constexpr int DB = D / 16;
   constexpr int KSTR = DK + 8;
   constexpr int TSTR = BN + 8;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[BN * KSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[BN * KSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Kt[D * TSTR];
+  constexpr int NBUF = D <= 64 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) bf16 Ks[NBUF][BN * KSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[NBUF][BN * KSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Kt[NBUF][D * TSTR];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
   const int N = p.N;
@@ -396,74 +479,81 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   const uint8_t* mrow =
       (p.mask && has_rows) ? p.mask + ((int64_t)bh * p.nq32 + (qrow0 >> 5)) * p.nk64 : nullptr;
 
+  PairTile<BN, D> kt, vt;
+#pragma unroll
+  for (int bb = 0; bb < NBUF; ++bb) {
+    zero_pad_cols<BN, D, DK, KSTR>(Ks[bb], tid);
+    zero_pad_cols<BN, D, DK, KSTR>(Vs[bb], tid);
+  }
+  kt.load(K, p.ksn, 0, N, tid);
+  vt.load(V, p.vsn, 0, N, tid);
+  kt.template store_rows<KSTR>(Ks[0], tid);
+  kt.template store_cols<TSTR>(Kt[0], tid);
+  vt.template store_rows<KSTR>(Vs[0], tid);
+
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = t * BN;
+    const int cur = NBUF == 2 ? (t & 1) : 0;
     __syncthreads();
-    stage_rows<BN, D, DK, KSTR>(Ks, K, p.ksn, n0, N, tid);
-    stage_rows<BN, D, DK, KSTR>(Vs, V, p.vsn, n0, N, tid);
-    stage_rows_t<BN, D, TSTR>(Kt, K, p.ksn, n0, N, tid);
-    __syncthreads();
-    if (!has_rows || (CAUSAL && n0 > qrow0 + 31)) continue;
-    if (mrow && mrow[t] == 0) continue;
-
-    f32x4 s[4][2], dw[4][2];
+    const bool pre = t + 1 < ntiles;
+    if (pre) {
+      kt.load(K, p.ksn, n0 + BN, N, tid);
+      vt.load(V, p.vsn, n0 + BN, N, tid);
+    }
+    const bool work = has_rows && !(CAUSAL && n0 > qrow0 + 31) && !(mrow && mrow[t] == 0);
+    if (work) {
+      const bf16* Kc = Ks[cur];
+      const bf16* Vc = Vs[cur];
+      const bf16* Ktc = Kt[cur];
+      const bool masked = (CAUSAL && n0 + BN - 1 > qrow0) || n0 + BN > N;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int kr = perm_row(kb, r16) * KSTR + 8 * g;
-      bf16x8 kf[KS], vf[KS];
+      for (int hf = 0; hf < 2; ++hf) {
+        if (CAUSAL && n0 + 32 * hf > qrow0 + 31) break;
+        f32x4 s[2][2], dw[2][2];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        kf[ks] = ld16(Ks + kr + 32 * ks);
-        vf[ks] = ld16(Vs + kr + 32 * ks);
-      }
+        for (int kk = 0; kk < 2; ++kk) {
+          const int kr = perm_row(2 * hf + kk, r16) * KSTR + 8 * g;
+          bf16x8 kf[KS], vf[KS];
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
+          for (int ks = 0; ks < KS; ++ks) {
+            kf[ks] = ld16(Kc + kr + 32 * ks);
+            vf[ks] = ld16(Vc + kr + 32 * ks);
+          }
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          a = mfma16x16x32(kf[ks], qf[qb][ks], a);
-          c = mfma16x16x32(vf[ks], dof[qb][ks], c);
+          for (int qb = 0; qb < 2; ++qb) {
+            f32x4 a4 = {0.f, 0.f, 0.f, 0.f}, c4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+              a4 = mfma16x16x32(kf[ks], qf[qb][ks], a4);
+              c4 = mfma16x16x32(vf[ks], dof[qb][ks], c4);
+            }
+            s[kk][qb] = a4;
+            dw[kk][qb] = c4;
+          }
         }
-        s[kb][qb] = a;
-        dw[kb][qb] = c;
+        if (masked)
+          ds_kq<true>(s, dw, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+        else
+          ds_kq<false>(s, dw, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+        bf16x8 pf[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+          pf[qb] = pack8(s[0][qb][0], s[0][qb][1], s[0][qb][2], s[0][qb][3], s[1][qb][0],
+                         s[1][qb][1], s[1][qb][2], s[1][qb][3]);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const bf16x8 ktf = ld16(Ktc + (16 * db + r16) * TSTR + 32 * hf + 8 * g);
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(ktf, pf[qb], acc[db][qb]);
+        }
       }
     }
-    const bool diag = CAUSAL && (n0 + BN - 1 > qrow0);
-    const bool edge = n0 + BN > N;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float sv = __builtin_fmaf(s[kb][qb][i], scale, ntau);
-          float u = sv > 0.f ? sv : 0.f;
-          if (diag || edge) {
-            const int key = n0 + perm_row(kb, 4 * g + i);
-            const int qrow = qrow0 + 16 * qb + r16;
-            if ((CAUSAL && key > qrow) || key >= N) u = 0.f;
-          }
-          const float u2 = u * u;
-          const float u4 = u2 * u2;
-          const float u9 = u4 * u4 * u;
-          float ds = rc[qb] * u9 * (dw[kb][qb][i] - rD[qb]);
-          if (u == rM[qb] && u > 0.f) ds += rG[qb];
-          s[kb][qb][i] = ds;
-        }
-#pragma unroll
-    for (int tp = 0; tp < 2; ++tp) {
-      bf16x8 pf[2];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-        pf[qb] = pack8(s[2 * tp][qb][0], s[2 * tp][qb][1], s[2 * tp][qb][2], s[2 * tp][qb][3],
-                       s[2 * tp + 1][qb][0], s[2 * tp + 1][qb][1], s[2 * tp + 1][qb][2],
-                       s[2 * tp + 1][qb][3]);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const bf16x8 kt = ld16(Kt + (16 * db + r16) * TSTR + 32 * tp + 8 * g);
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(kt, pf[qb], acc[db][qb]);
-      }
+    if (pre) {
+      if (NBUF == 1) __syncthreads();
+      const int nxt = NBUF == 2 ? cur ^ 1 : 0;
+      kt.template store_rows<KSTR>(Ks[nxt], tid);
+      kt.template store_cols<TSTR>(Kt[nxt], tid);
+      vt.template store_rows<KSTR>(Vs[nxt], tid);
     }
   }
 
@@ -493,6 +583,45 @@ struct DkdvCfg {
   static constexpr int BNK = 4 * KPW;
 };
 
+// In the S layout (key per lane, four query rows per 16-row block), for one 32-row half
+// (query blocks 2*hf, 2*hf+1): w = u^10 g/Z written over s and ds written over dw; returns
+// the lane's sum of ds.
+template <bool MASK, int KB>
+__device__ __forceinline__ float w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const f32x4* RCc,
+                                         float scale, float ntau, int m0, int hf, int kw0, int N,
+                                         bool causal, int g, int r16) {
+  float tsum = 0.f;
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int lr = perm_row(2 * hf + qq, 4 * g + i);
+      const f32x4 c0 = RCc[2 * lr];
+      const float rM = c0[0], rr = c0[1], rcoef = c0[2], rD = c0[3];
+      const float rG = RCc[2 * lr + 1][0];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        float u = fmaxf(__builtin_fmaf(s[qq][kb][i], scale, ntau), 0.f);
+        if (MASK) {
+          const int qrow = m0 + lr;
+          const int key = kw0 + 16 * kb + r16;
+          if ((causal && key > qrow) || key >= N || qrow >= N) u = 0.f;
+        }
+        const float u2 = u * u;
+        const float u4 = u2 * u2;
+        const float u8 = u4 * u4;
+        const float u9 = u8 * u;
+        s[qq][kb][i] = u8 * u2 * rr;  // w = P g / Z
+        const float tie = (u == rM) ? rG : 0.f;
+        const float ds = __builtin_fmaf(rcoef * u9, dw[qq][kb][i] - rD, tie);
+        dw[qq][kb][i] = ds;
+        tsum += ds;
+      }
+    }
+  }
+  return tsum;
+}
+
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   constexpr int KPW = DkdvCfg<D>::KPW, KB = DkdvCfg<D>::KB, BNK = DkdvCfg<D>::BNK;
@@ -502,11 +631,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   constexpr int DB = D / 16;
   constexpr int QSTR = DK + 8;
   constexpr int TSTR = BMQ + 8;
-  __shared__ __attribute__((aligned(16))) bf16 Qs[BMQ * QSTR];
-  __shared__ __attribute__((aligned(16))) bf16 dOs[BMQ * QSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Qt[D * TSTR];
-  __shared__ __attribute__((aligned(16))) bf16 dOt[D * TSTR];
-  __shared__ __attribute__((aligned(16))) f32x4 RC[BMQ * 2];
+  constexpr int NBUF = D <= 64 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) bf16 Qs[NBUF][BMQ * QSTR];
+  __shared__ __attribute__((aligned(16))) bf16 dOs[NBUF][BMQ * QSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Qt[NBUF][D * TSTR];
+  __shared__ __attribute__((aligned(16))) bf16 dOt[NBUF][D * TSTR];
+  __shared__ __attribute__((aligned(16))) f32x4 RC[NBUF][BMQ * 2];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
   const int N = p.N;
@@ -517,6 +647,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const bf16* K = static_cast<const bf16*>(p.k) + b * p.ksb + h * p.ksh;
   const bf16* V = static_cast<const bf16*>(p.v) + b * p.vsb + h * p.vsh;
   const bf16* dO = static_cast<const bf16*>(p.dout) + b * p.dosb + h * p.dosh;
+  const f32x4* RCg = reinterpret_cast<const f32x4*>(p.rc) + 2 * (int64_t)bh * N;
   const int kv0 = kvb * BNK;
   const int kw0 = kv0 + KPW * w;
   const bool has_keys = kw0 < N;
@@ -550,104 +681,106 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const int ktile = kw0 >> 6;  // 64-key tile of this wave's keys (forward mask column)
   const uint8_t* mcol = (p.mask && has_keys) ? p.mask + (int64_t)bh * p.nq32 * p.nk64 + ktile : nullptr;
 
+  PairTile<BMQ, D> qtl, otl;
+  f32x4 rcr = {0.f, 0.f, 0.f, 0.f};
+  auto load_tile = [&](int m) {
+    qtl.load(Q, p.qsn, m, N, tid);
+    otl.load(dO, p.dosn, m, N, tid);
+    if (tid < 2 * BMQ) {
+      const int row = m + (tid >> 1);
+      rcr = row < N ? RCg[2 * row + (tid & 1)] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto store_tile = [&](int bb) {
+    qtl.template store_rows<QSTR>(Qs[bb], tid);
+    qtl.template store_cols<TSTR>(Qt[bb], tid);
+    otl.template store_rows<QSTR>(dOs[bb], tid);
+    otl.template store_cols<TSTR>(dOt[bb], tid);
+    if (tid < 2 * BMQ) RC[bb][tid] = rcr;
+  };
+#pragma unroll
+  for (int bb = 0; bb < NBUF; ++bb) {
+    zero_pad_cols<BMQ, D, DK, QSTR>(Qs[bb], tid);
+    zero_pad_cols<BMQ, D, DK, QSTR>(dOs[bb], tid);
+  }
+  if (qt0 < nqt) {
+    load_tile(qt0 * BMQ);
+    store_tile(0);
+  }
+
   for (int qt = qt0; qt < nqt; ++qt) {
     const int m0 = qt * BMQ;
+    const int cur = NBUF == 2 ? ((qt - qt0) & 1) : 0;
     __syncthreads();
-    stage_rows<BMQ, D, DK, QSTR>(Qs, Q, p.qsn, m0, N, tid);
-    stage_rows<BMQ, D, DK, QSTR>(dOs, dO, p.dosn, m0, N, tid);
-    stage_rows_t<BMQ, D, TSTR>(Qt, Q, p.qsn, m0, N, tid);
-    stage_rows_t<BMQ, D, TSTR>(dOt, dO, p.dosn, m0, N, tid);
-    if (tid < 2 * BMQ) {
-      const int row = m0 + (tid >> 1);
-      RC[tid] = row < N ? reinterpret_cast<const f32x4*>(p.rc)[2 * ((int64_t)bh * N + row) + (tid & 1)]
-                        : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    __syncthreads();
-    if (!has_keys || (CAUSAL && m0 + BMQ - 1 < kw0)) continue;
-    if (mcol) {
+    const bool pre = qt + 1 < nqt;
+    if (pre) load_tile(m0 + BMQ);
+    bool work = has_keys && !(CAUSAL && m0 + BMQ - 1 < kw0);
+    if (work && mcol) {
       const int r32 = m0 >> 5;
       const bool a0 = mcol[(int64_t)r32 * p.nk64] != 0;
       const bool a1 = (r32 + 1 < p.nq32) && mcol[(int64_t)(r32 + 1) * p.nk64] != 0;
-      if (!a0 && !a1) continue;
+      work = a0 || a1;
     }
-
-    f32x4 s[4][KB], dw[4][KB];
+    if (work) {
+      const bf16* Qc = Qs[cur];
+      const bf16* dOc = dOs[cur];
+      const bf16* Qtc = Qt[cur];
+      const bf16* dOtc = dOt[cur];
+      const bool masked = (CAUSAL && m0 < kw0 + KPW - 1) || m0 + BMQ > N || kw0 + KPW > N;
+      float tsum = 0.f;
 #pragma unroll
-    for (int qb = 0; qb < 4; ++qb) {
-      const int qr = perm_row(qb, r16) * QSTR + 8 * g;
-      bf16x8 qa[KS], da[KS];
+      for (int hf = 0; hf < 2; ++hf) {
+        if (CAUSAL && m0 + 32 * hf + 31 < kw0) continue;  // rows of this half precede the keys
+        f32x4 s[2][KB], dw[2][KB];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        qa[ks] = ld16(Qs + qr + 32 * ks);
-        da[ks] = ld16(dOs + qr + 32 * ks);
-      }
+        for (int qq = 0; qq < 2; ++qq) {
+          const int qr = perm_row(2 * hf + qq, r16) * QSTR + 8 * g;
+          bf16x8 qa[KS], da[KS];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        f32x4 a = {0.f, 0.f, 0.f, 0.f}, c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          a = mfma16x16x32(qa[ks], kf[kb][ks], a);
-          c = mfma16x16x32(da[ks], vf[kb][ks], c);
-        }
-        s[qb][kb] = a;
-        dw[qb][kb] = c;
-      }
-    }
-    const bool diag = CAUSAL && (m0 < kw0 + KPW - 1);
-    const bool edge = m0 + BMQ > N || kw0 + KPW > N;
-    float tsum = 0.f;
-#pragma unroll
-    for (int qb = 0; qb < 4; ++qb) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int lr = perm_row(qb, 4 * g + i);
-        const f32x4 c0 = RC[2 * lr];
-        const float rM = c0[0], rr = c0[1], rcoef = c0[2], rD = c0[3];
-        const float rG = RC[2 * lr + 1][0];
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          const float sv = __builtin_fmaf(s[qb][kb][i], scale, ntau);
-          float u = sv > 0.f ? sv : 0.f;
-          if (diag || edge) {
-            const int qrow = m0 + lr;
-            const int key = kw0 + 16 * kb + r16;
-            if ((CAUSAL && key > qrow) || key >= N || qrow >= N) u = 0.f;
+          for (int ks = 0; ks < KS; ++ks) {
+            qa[ks] = ld16(Qc + qr + 32 * ks);
+            da[ks] = ld16(dOc + qr + 32 * ks);
           }
-          const float u2 = u * u;
-          const float u4 = u2 * u2;
-          const float u8 = u4 * u4;
-          const float u9 = u8 * u;
-          s[qb][kb][i] = u8 * u2 * rr;  // w = P g / Z
-          float ds = rcoef * u9 * (dw[qb][kb][i] - rD);
-          if (u == rM && u > 0.f) ds += rG;
-          dw[qb][kb][i] = ds;
-          tsum += ds;
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            f32x4 a4 = {0.f, 0.f, 0.f, 0.f}, c4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+              a4 = mfma16x16x32(qa[ks], kf[kb][ks], a4);
+              c4 = mfma16x16x32(da[ks], vf[kb][ks], c4);
+            }
+            s[qq][kb] = a4;
+            dw[qq][kb] = c4;
+          }
         }
-      }
-    }
-    dsum += (double)tsum;
-#pragma unroll
-    for (int tp = 0; tp < 2; ++tp) {
-      bf16x8 wf[KB], sf[KB];
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        wf[kb] = pack8(s[2 * tp][kb][0], s[2 * tp][kb][1], s[2 * tp][kb][2], s[2 * tp][kb][3],
-                       s[2 * tp + 1][kb][0], s[2 * tp + 1][kb][1], s[2 * tp + 1][kb][2],
-                       s[2 * tp + 1][kb][3]);
-        sf[kb] = pack8(dw[2 * tp][kb][0], dw[2 * tp][kb][1], dw[2 * tp][kb][2], dw[2 * tp][kb][3],
-                       dw[2 * tp + 1][kb][0], dw[2 * tp + 1][kb][1], dw[2 * tp + 1][kb][2],
-                       dw[2 * tp + 1][kb][3]);
-      }
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const bf16x8 ot = ld16(dOt + (16 * db + r16) * TSTR + 32 * tp + 8 * g);
-        const bf16x8 qt_ = ld16(Qt + (16 * db + r16) * TSTR + 32 * tp + 8 * g);
+        if (masked)
+          tsum += w_ds_qk<true, KB>(s, dw, RC[cur], scale, ntau, m0, hf, kw0, N, CAUSAL, g, r16);
+        else
+          tsum += w_ds_qk<false, KB>(s, dw, RC[cur], scale, ntau, m0, hf, kw0, N, CAUSAL, g, r16);
+        bf16x8 wf[KB], sf[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          adv[db][kb] = mfma16x16x32(ot, wf[kb], adv[db][kb]);
-          adk[db][kb] = mfma16x16x32(qt_, sf[kb], adk[db][kb]);
+          wf[kb] = pack8(s[0][kb][0], s[0][kb][1], s[0][kb][2], s[0][kb][3], s[1][kb][0],
+                         s[1][kb][1], s[1][kb][2], s[1][kb][3]);
+          sf[kb] = pack8(dw[0][kb][0], dw[0][kb][1], dw[0][kb][2], dw[0][kb][3], dw[1][kb][0],
+                         dw[1][kb][1], dw[1][kb][2], dw[1][kb][3]);
+        }
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const bf16x8 ot = ld16(dOtc + (16 * db + r16) * TSTR + 32 * hf + 8 * g);
+          const bf16x8 qt_ = ld16(Qtc + (16 * db + r16) * TSTR + 32 * hf + 8 * g);
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            adv[db][kb] = mfma16x16x32(ot, wf[kb], adv[db][kb]);
+            adk[db][kb] = mfma16x16x32(qt_, sf[kb], adk[db][kb]);
+          }
         }
       }
+      dsum += (double)tsum;
+    }
+    if (pre) {
+      if (NBUF == 1) __syncthreads();
+      store_tile(NBUF == 2 ? cur ^ 1 : 0);
     }
   }
 
