@@ -38,17 +38,72 @@ __device__ __forceinline__ int perm_row(int blk, int r) {
 
 __device__ __forceinline__ bf16x8 ld16(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
+// LDS tiles are unpadded and XOR-swizzled on the 16-byte chunk index of each row.  The
+// swizzles are linear over GF(2) in the row bits and were chosen (exhaustive model of the
+// access patterns, 32- and 64-bank LDS) so that the MFMA fragment reads are conflict free
+// and the staging stores at most 2-way:
+//  * row-major tiles [rows][DK] are read as 16 permuted rows x 4 chunk groups;
+//  * transposed tiles [D][64] are read as 16 consecutive rows x 4 chunk groups and written
+//    one 4-byte key pair at a time.
+// Linearity lets a fragment's swizzle split into a per-lane part and a compile-time part.
+__device__ __forceinline__ constexpr int parity6(int x) { return __builtin_popcount(x & 63) & 1; }
+__device__ __forceinline__ constexpr int swz_rows(int row) {
+  return parity6(row & 41) | (parity6(row & 52) << 1) | (parity6(row & 42) << 2);
+}
+__device__ __forceinline__ constexpr int swz_cols(int d) {
+  return parity6(d & 18) | (parity6(d & 39) << 1) | (parity6(d & 12) << 2);
+}
+template <int DK>
+__device__ __forceinline__ constexpr int chunk_mask() {
+  return (DK / 8 < 8 ? DK / 8 : 8) - 1;
+}
+
+// Element offset of 16-byte chunk `chunk` of row `row` in a row-major tile of DK columns.
+template <int DK>
+__device__ __forceinline__ int rt_off(int row, int chunk) {
+  return row * DK + ((chunk ^ (swz_rows(row) & chunk_mask<DK>())) << 3);
+}
+// Element offset of keys 8*kc .. 8*kc+7 of row d in a transposed [D][64] tile.
+__device__ __forceinline__ int tt_off(int d, int kc) { return d * 64 + ((kc ^ swz_cols(d)) << 3); }
+
+// Fragment addressing with the lane part hoisted.  A row-major fragment reads row
+// perm_row(blk, r16) = rowc(blk) + rowl(r16) (disjoint bits) at chunk g + 4*ks:
+//   offset = rowc*DK + rowl*DK + (((g ^ swz(rowl)) ^ (4*ks ^ swz(rowc))) << 3).
+struct FragLane {
+  int rbase;  // rowl * DK   (row-major) or r16 * 64 (transposed)
+  int x;      // g ^ swizzle(lane row part)
+};
+template <int DK>
+__device__ __forceinline__ FragLane rt_lane(int r16, int g) {
+  const int rowl = 8 * (r16 >> 2) + (r16 & 3);
+  return FragLane{rowl * DK, g ^ (swz_rows(rowl) & chunk_mask<DK>())};
+}
+template <int DK>
+__device__ __forceinline__ int rt_frag(const FragLane& fl, int blk, int ks) {
+  const int rowc = 32 * (blk >> 1) + 4 * (blk & 1);
+  const int cc = (4 * ks) ^ (swz_rows(rowc) & chunk_mask<DK>());
+  return rowc * DK + fl.rbase + ((fl.x ^ cc) << 3);
+}
+__device__ __forceinline__ FragLane tt_lane(int r16, int g) {
+  return FragLane{r16 * 64, g ^ swz_cols(r16)};
+}
+__device__ __forceinline__ int tt_frag(const FragLane& fl, int db, int hf) {
+  const int cc = (4 * hf) ^ swz_cols(16 * db);
+  return 16 * db * 64 + fl.rbase + ((fl.x ^ cc) << 3);
+}
+
 // Register-staged copy of rows [row0, row0 + ROWS) of an [N, D] bf16 slice (row stride sn).
 // Chunk c of a thread covers rows 2*(c / CPR) and 2*(c / CPR) + 1 at columns
 // 8*(c % CPR) .. +7 (CPR = D/8 chunks per row), so a wave's load instruction reads whole
 // contiguous rows.  load() issues the global reads into registers (rows >= N read as zero);
-// store_rows() writes them row-major (row stride STR) and store_cols() transposed
-// (dst[col * STR + row]) -- one global read serves both LDS layouts.
+// store_rows() writes them to a row-major tile and store_cols() to a transposed [D][ROWS]
+// tile -- one global read serves both LDS layouts.
 template <int ROWS, int D>
 struct PairTile {
   static constexpr int CPR = D / 8;
   static constexpr int NCH = (ROWS / 2) * CPR;
   static constexpr int PER = (NCH + 255) / 256;
+  static_assert(ROWS == 64, "transposed tiles are 64 keys/rows wide");
   u32x4 a[PER], b[PER];
 
   __device__ __forceinline__ void load(const bf16* src, int64_t sn, int row0, int N, int tid) {
@@ -64,19 +119,18 @@ struct PairTile {
       }
     }
   }
-  template <int STR>
+  template <int DK>
   __device__ __forceinline__ void store_rows(bf16* dst, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + 256 * i;
       if (NCH % 256 == 0 || c < NCH) {
-        const int r = 2 * (c / CPR), col = 8 * (c % CPR);
-        *reinterpret_cast<u32x4*>(dst + r * STR + col) = a[i];
-        *reinterpret_cast<u32x4*>(dst + (r + 1) * STR + col) = b[i];
+        const int r = 2 * (c / CPR), ch = c % CPR;
+        *reinterpret_cast<u32x4*>(dst + rt_off<DK>(r, ch)) = a[i];
+        *reinterpret_cast<u32x4*>(dst + rt_off<DK>(r + 1, ch)) = b[i];
       }
     }
   }
-  template <int STR>
   __device__ __forceinline__ void store_cols(bf16* dst, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -87,20 +141,21 @@ struct PairTile {
         for (int e = 0; e < 8; ++e) {
           const uint32_t lo = (e & 1) ? (a[i][e >> 1] >> 16) : (a[i][e >> 1] & 0xffffu);
           const uint32_t hi = (e & 1) ? (b[i][e >> 1] & 0xffff0000u) : (b[i][e >> 1] << 16);
-          *reinterpret_cast<uint32_t*>(dst + (col + e) * STR + r) = lo | hi;
+          *reinterpret_cast<uint32_t*>(dst + tt_off(col + e, r >> 3) + (r & 7)) = lo | hi;
         }
       }
     }
   }
 };
 
-// Zero columns [D, DK) of a row-major LDS tile (the k-padding of the 32-wide MFMA when D < 32).
-template <int ROWS, int D, int DK, int STR>
+// Zero the k-padding chunks [D/8, DK/8) of a row-major tile (the 32-wide MFMA when D < 32).
+template <int ROWS, int D, int DK>
 __device__ __forceinline__ void zero_pad_cols(bf16* dst, int tid) {
   if (D < DK) {
-    for (int c = tid; c < ROWS * ((DK - D) / 8); c += 256) {
-      const int r = c / ((DK - D) / 8), col = D + 8 * (c % ((DK - D) / 8));
-      *reinterpret_cast<u32x4*>(dst + r * STR + col) = u32x4{0u, 0u, 0u, 0u};
+    constexpr int PC = (DK - D) / 8;
+    for (int c = tid; c < ROWS * PC; c += 256) {
+      const int r = c / PC, ch = D / 8 + c % PC;
+      *reinterpret_cast<u32x4*>(dst + rt_off<DK>(r, ch)) = u32x4{0u, 0u, 0u, 0u};
     }
   }
 }
@@ -158,10 +213,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
-  constexpr int KSTR = DK + 8;
-  constexpr int VSTR = BN + 8;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][BN * KSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Vt[2][D * VSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Ks[2][BN * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Vt[2][D * BN];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
   const int N = p.N;
@@ -177,6 +230,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
   const bool has_rows = qrow0 < N;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
+  const FragLane flr = rt_lane<DK>(r16, g), flt = tt_lane(r16, g);
 
   bf16x8 qf[2][KS];
 #pragma unroll
@@ -215,12 +269,12 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
   // Software pipeline: tile t+1 is read from HBM/L2 into registers while tile t is
   // computed from LDS, then committed to the other LDS buffer; one barrier per tile.
   PairTile<BN, D> kt, vt;
-  zero_pad_cols<BN, D, DK, KSTR>(Ks[0], tid);
-  zero_pad_cols<BN, D, DK, KSTR>(Ks[1], tid);
+  zero_pad_cols<BN, D, DK>(Ks[0], tid);
+  zero_pad_cols<BN, D, DK>(Ks[1], tid);
   kt.load(K, p.ksn, 0, N, tid);
   vt.load(V, p.vsn, 0, N, tid);
-  kt.template store_rows<KSTR>(Ks[0], tid);
-  vt.template store_cols<VSTR>(Vt[0], tid);
+  kt.template store_rows<DK>(Ks[0], tid);
+  vt.store_cols(Vt[0], tid);
 
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = t * BN;
@@ -243,10 +297,9 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
         f32x4 s[2][2];
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const bf16* kr = Kc + perm_row(2 * hf + kk, r16) * KSTR + 8 * g;
           bf16x8 kf[KS];
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) kf[ks] = ld16(kr + 32 * ks);
+          for (int ks = 0; ks < KS; ++ks) kf[ks] = ld16(Kc + rt_frag<DK>(flr, 2 * hf + kk, ks));
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
             f32x4 a4 = {0.f, 0.f, 0.f, 0.f};
@@ -279,7 +332,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
         }
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16x8 vf = ld16(Vc + (16 * db + r16) * VSTR + 32 * hf + 8 * g);
+          const bf16x8 vf = ld16(Vc + tt_frag(flt, db, hf));
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(vf, pf[qb], acc[db][qb]);
         }
@@ -290,8 +343,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
     }
     if (mrow && lane == 0) mrow[t] = active ? 1 : 0;
     if (pre) {
-      kt.template store_rows<KSTR>(Ks[cur ^ 1], tid);
-      vt.template store_cols<VSTR>(Vt[cur ^ 1], tid);
+      kt.template store_rows<DK>(Ks[cur ^ 1], tid);
+      vt.store_cols(Vt[cur ^ 1], tid);
     }
   }
   if (mrow && lane == 0)
@@ -422,12 +475,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
-  constexpr int KSTR = DK + 8;
-  constexpr int TSTR = BN + 8;
   constexpr int NBUF = D <= 64 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[NBUF][BN * KSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[NBUF][BN * KSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Kt[NBUF][D * TSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Ks[NBUF][BN * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[NBUF][BN * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Kt[NBUF][D * BN];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
   const int N = p.N;
@@ -444,6 +495,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   const bool has_rows = qrow0 < N;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
+  const FragLane flr = rt_lane<DK>(r16, g), flt = tt_lane(r16, g);
 
   bf16x8 qf[2][KS], dof[2][KS];
   float rM[2], rc[2], rD[2], rG[2];
@@ -482,14 +534,14 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   PairTile<BN, D> kt, vt;
 #pragma unroll
   for (int bb = 0; bb < NBUF; ++bb) {
-    zero_pad_cols<BN, D, DK, KSTR>(Ks[bb], tid);
-    zero_pad_cols<BN, D, DK, KSTR>(Vs[bb], tid);
+    zero_pad_cols<BN, D, DK>(Ks[bb], tid);
+    zero_pad_cols<BN, D, DK>(Vs[bb], tid);
   }
   kt.load(K, p.ksn, 0, N, tid);
   vt.load(V, p.vsn, 0, N, tid);
-  kt.template store_rows<KSTR>(Ks[0], tid);
-  kt.template store_cols<TSTR>(Kt[0], tid);
-  vt.template store_rows<KSTR>(Vs[0], tid);
+  kt.template store_rows<DK>(Ks[0], tid);
+  kt.store_cols(Kt[0], tid);
+  vt.template store_rows<DK>(Vs[0], tid);
 
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = t * BN;
@@ -512,12 +564,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
         f32x4 s[2][2], dw[2][2];
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const int kr = perm_row(2 * hf + kk, r16) * KSTR + 8 * g;
           bf16x8 kf[KS], vf[KS];
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
-            kf[ks] = ld16(Kc + kr + 32 * ks);
-            vf[ks] = ld16(Vc + kr + 32 * ks);
+            const int off = rt_frag<DK>(flr, 2 * hf + kk, ks);
+            kf[ks] = ld16(Kc + off);
+            vf[ks] = ld16(Vc + off);
           }
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
@@ -542,7 +594,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
                          s[1][qb][1], s[1][qb][2], s[1][qb][3]);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16x8 ktf = ld16(Ktc + (16 * db + r16) * TSTR + 32 * hf + 8 * g);
+          const bf16x8 ktf = ld16(Ktc + tt_frag(flt, db, hf));
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(ktf, pf[qb], acc[db][qb]);
         }
@@ -551,9 +603,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
     if (pre) {
       if (NBUF == 1) __syncthreads();
       const int nxt = NBUF == 2 ? cur ^ 1 : 0;
-      kt.template store_rows<KSTR>(Ks[nxt], tid);
-      kt.template store_cols<TSTR>(Kt[nxt], tid);
-      vt.template store_rows<KSTR>(Vs[nxt], tid);
+      kt.template store_rows<DK>(Ks[nxt], tid);
+      kt.store_cols(Kt[nxt], tid);
+      vt.template store_rows<DK>(Vs[nxt], tid);
     }
   }
 
@@ -629,13 +681,11 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
-  constexpr int QSTR = DK + 8;
-  constexpr int TSTR = BMQ + 8;
   constexpr int NBUF = D <= 64 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) bf16 Qs[NBUF][BMQ * QSTR];
-  __shared__ __attribute__((aligned(16))) bf16 dOs[NBUF][BMQ * QSTR];
-  __shared__ __attribute__((aligned(16))) bf16 Qt[NBUF][D * TSTR];
-  __shared__ __attribute__((aligned(16))) bf16 dOt[NBUF][D * TSTR];
+  __shared__ __attribute__((aligned(16))) bf16 Qs[NBUF][BMQ * DK];
+  __shared__ __attribute__((aligned(16))) bf16 dOs[NBUF][BMQ * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Qt[NBUF][D * BMQ];
+  __shared__ __attribute__((aligned(16))) bf16 dOt[NBUF][D * BMQ];
   __shared__ __attribute__((aligned(16))) f32x4 RC[NBUF][BMQ * 2];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
@@ -653,6 +703,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const bool has_keys = kw0 < N;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
+  const FragLane flr = rt_lane<DK>(r16, g), flt = tt_lane(r16, g);
 
   bf16x8 kf[KB][KS], vf[KB][KS];
 #pragma unroll
@@ -692,16 +743,16 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     }
   };
   auto store_tile = [&](int bb) {
-    qtl.template store_rows<QSTR>(Qs[bb], tid);
-    qtl.template store_cols<TSTR>(Qt[bb], tid);
-    otl.template store_rows<QSTR>(dOs[bb], tid);
-    otl.template store_cols<TSTR>(dOt[bb], tid);
+    qtl.template store_rows<DK>(Qs[bb], tid);
+    qtl.store_cols(Qt[bb], tid);
+    otl.template store_rows<DK>(dOs[bb], tid);
+    otl.store_cols(dOt[bb], tid);
     if (tid < 2 * BMQ) RC[bb][tid] = rcr;
   };
 #pragma unroll
   for (int bb = 0; bb < NBUF; ++bb) {
-    zero_pad_cols<BMQ, D, DK, QSTR>(Qs[bb], tid);
-    zero_pad_cols<BMQ, D, DK, QSTR>(dOs[bb], tid);
+    zero_pad_cols<BMQ, D, DK>(Qs[bb], tid);
+    zero_pad_cols<BMQ, D, DK>(dOs[bb], tid);
   }
   if (qt0 < nqt) {
     load_tile(qt0 * BMQ);
@@ -734,12 +785,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         f32x4 s[2][KB], dw[2][KB];
 #pragma unroll
         for (int qq = 0; qq < 2; ++qq) {
-          const int qr = perm_row(2 * hf + qq, r16) * QSTR + 8 * g;
           bf16x8 qa[KS], da[KS];
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
-            qa[ks] = ld16(Qc + qr + 32 * ks);
-            da[ks] = ld16(dOc + qr + 32 * ks);
+            const int off = rt_frag<DK>(flr, 2 * hf + qq, ks);
+            qa[ks] = ld16(Qc + off);
+            da[ks] = ld16(dOc + off);
           }
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
@@ -767,8 +818,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         }
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16x8 ot = ld16(dOtc + (16 * db + r16) * TSTR + 32 * hf + 8 * g);
-          const bf16x8 qt_ = ld16(Qtc + (16 * db + r16) * TSTR + 32 * hf + 8 * g);
+          const int toff = tt_frag(flt, db, hf);
+          const bf16x8 ot = ld16(dOtc + toff);
+          const bf16x8 qt_ = ld16(Qtc + toff);
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
             adv[db][kb] = mfma16x16x32(ot, wf[kb], adv[db][kb]);
