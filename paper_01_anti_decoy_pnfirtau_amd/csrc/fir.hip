@@ -1,11 +1,14 @@
 // Causal depthwise FIR along the sequence axis (keys of pn_fir_tau), forward and adjoint.
 //
-// Streaming, HBM-bound.  Each thread owns one 16-byte channel chunk of RUN consecutive
+// Streaming, HBM-bound.  Each thread owns one 16-byte channel chunk of RUN = 8 consecutive
 // sequence rows of one (b, h) slice: it issues all RUN + K - 1 row loads up front (the
-// causal halo of K - 1 rows is re-read from L2 by the neighbouring run), evaluates the
-// fp32 fused multiply-add chain in lag order and writes RUN 16-byte rows.  Eight
-// consecutive lanes cover one 128-byte row of a d = 64 bf16 head, so every load and
-// store instruction touches whole cache lines.
+// K - 1 row causal halo is served by L2: the neighbouring run of the same wave reads those
+// rows at the same time), evaluates the fp32 fused multiply-add chain in lag order and
+// writes RUN 16-byte rows with non-temporal stores (the output is streamed, not re-read by
+// this kernel).  Eight consecutive lanes cover one 128-byte row of a d = 64 bf16 head, so
+// every load and store instruction moves whole cache lines.  Of the variants measured on
+// MI355X (runs of 2..64 rows, an LDS-staged 64-row tile, non-temporal loads), this one is
+// the fastest and matches a plain device copy of the same bytes.
 //
 // Numerics follow src/triton_pnfirtau.py:72-84 (forward) and :120-132 (adjoint):
 // acc = x[n] * h0; acc = fma(x[n -/+ u], h_u, acc) for u = 1..K-1 while in range;
@@ -15,7 +18,7 @@
 namespace pnfx {
 namespace {
 
-constexpr int RUN = 16;
+constexpr int RUN = 8;
 constexpr int KMAX = 16;
 
 template <typename T>
@@ -23,8 +26,7 @@ struct Chunk {
   static constexpr int VEC = 16 / sizeof(T);
 };
 
-// A 16-byte chunk is kept raw in registers (4 dwords) and widened to fp32 on use, so a
-// window of RUN + K - 1 rows costs 4 VGPRs per row.
+// A 16-byte chunk is kept raw (4 dwords) and widened to fp32 on use.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
@@ -46,14 +48,14 @@ __device__ __forceinline__ void store_chunk<bf16>(bf16* p, const float* in) {
   bf16x8 v;
 #pragma unroll
   for (int e = 0; e < 8; ++e) v[e] = (bf16)in[e];
-  *reinterpret_cast<bf16x8*>(p) = v;
+  __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(p));
 }
 template <>
 __device__ __forceinline__ void store_chunk<float>(float* p, const float* in) {
   f32x4 v;
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = in[e];
-  *reinterpret_cast<f32x4*>(p) = v;
+  __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
 }
 
 struct FirArgs {
@@ -67,19 +69,21 @@ struct FirArgs {
 };
 
 // KT is the compile-time bound on the tap count (K <= KT); KT == 7 is the pn_fir_tau case.
+// grid.x covers the (run, chunk) pairs of one (b, h) slice, grid.y = b * H + h; all index
+// arithmetic except the final address is 32-bit (sizes are checked on the host).
 template <typename T, int KT, bool ADJ>
 __global__ __launch_bounds__(256) void fir_vec_kernel(FirArgs a) {
   constexpr int VEC = Chunk<T>::VEC;
   constexpr int WIN = RUN + KT - 1;
-  const int64_t CH = a.C / VEC;
-  const int64_t NR = (a.N + RUN - 1) / RUN;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= a.B * a.H * NR * CH) return;
-  const int64_t ch = t % CH;
-  const int64_t rest = t / CH;
-  const int64_t run = rest % NR;
-  const int64_t bh = rest / NR;
-  const int64_t b = bh / a.H, hh = bh % a.H;
+  const int CH = (int)a.C / VEC;
+  const int N = (int)a.N;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= ((N + RUN - 1) / RUN) * CH) return;
+  const int ch = t % CH;
+  const int run = t / CH;
+  const int bh = blockIdx.y;
+  const int H = (int)a.H;
+  const int b = bh / H, hh = bh % H;
   const int K = KT == 7 ? 7 : a.K;
 
   float h[KT];
@@ -87,32 +91,32 @@ __global__ __launch_bounds__(256) void fir_vec_kernel(FirArgs a) {
 #pragma unroll
   for (int u = 0; u < KT; ++u) h[u] = u < K ? tp[K - 1 - u] : 0.0f;
 
-  const T* xs = reinterpret_cast<const T*>(a.x) + b * a.sb + hh * a.sh + ch * VEC;
-  const int64_t n0 = run * RUN;
+  const T* xs = reinterpret_cast<const T*>(a.x) + (int64_t)b * a.sb + (int64_t)hh * a.sh + ch * VEC;
+  const int n0 = run * RUN;
   // Window row w holds sequence row m = base + w.
-  const int64_t base = ADJ ? n0 : n0 - (KT - 1);
+  const int base = ADJ ? n0 : n0 - (KT - 1);
   u32x4 win[WIN];
 #pragma unroll
   for (int w = 0; w < WIN; ++w) {
-    const int64_t m = base + w;
-    if (m >= 0 && m < a.N) {
-      win[w] = *reinterpret_cast<const u32x4*>(xs + m * a.sn);
+    const int m = base + w;
+    if (m >= 0 && m < N) {
+      win[w] = *reinterpret_cast<const u32x4*>(xs + (int64_t)m * a.sn);
     } else {
       win[w] = u32x4{0u, 0u, 0u, 0u};
     }
   }
-  T* ys = reinterpret_cast<T*>(a.y) + (bh * a.N) * a.C + ch * VEC;
+  T* ys = reinterpret_cast<T*>(a.y) + ((int64_t)bh * N + n0) * a.C + ch * VEC;
 #pragma unroll
   for (int j = 0; j < RUN; ++j) {
-    const int64_t n = n0 + j;
-    if (n < a.N) {
+    const int n = n0 + j;
+    if (n < N) {
       float acc[VEC];
       const int w0 = ADJ ? j : j + KT - 1;  // window index of row n
 #pragma unroll
       for (int e = 0; e < VEC; ++e) acc[e] = chunk_elem<T>(win[w0], e) * h[0];
 #pragma unroll
       for (int u = 1; u < KT; ++u) {
-        const bool ok = (u < K) && (ADJ ? (n + u < a.N) : (n - u >= 0));
+        const bool ok = (u < K) && (ADJ ? (n + u < N) : (n - u >= 0));
         if (ok) {
           const int wu = ADJ ? w0 + u : w0 - u;
 #pragma unroll
@@ -120,7 +124,7 @@ __global__ __launch_bounds__(256) void fir_vec_kernel(FirArgs a) {
             acc[e] = __builtin_fmaf(chunk_elem<T>(win[wu], e), h[u], acc[e]);
         }
       }
-      store_chunk<T>(ys + n * a.C, acc);
+      store_chunk<T>(ys + (int64_t)j * a.C, acc);
     }
   }
 }
@@ -151,14 +155,13 @@ int launch_fir(const FirArgs& a, hipStream_t st) {
   const bool vec_ok = (reinterpret_cast<uintptr_t>(a.x) % 16 == 0) &&
                       (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && a.C % VEC == 0 &&
                       a.sb % VEC == 0 && a.sh % VEC == 0 && a.sn % VEC == 0;
-  if (vec_ok) {
-    const int64_t NR = (a.N + RUN - 1) / RUN;
-    const int64_t total = a.B * a.H * NR * (a.C / VEC);
-    const int64_t blocks = (total + 255) / 256;
+  const int64_t per_slice = ((a.N + RUN - 1) / RUN) * (a.C / VEC);
+  if (vec_ok && per_slice < (1ll << 30) && a.B * a.H < 65536 && a.N < (1ll << 30)) {
+    const dim3 grid((unsigned)((per_slice + 255) / 256), (unsigned)(a.B * a.H));
     if (a.K == 7)
-      hipLaunchKernelGGL((fir_vec_kernel<T, 7, ADJ>), dim3(blocks), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((fir_vec_kernel<T, 7, ADJ>), grid, dim3(256), 0, st, a);
     else
-      hipLaunchKernelGGL((fir_vec_kernel<T, KMAX, ADJ>), dim3(blocks), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((fir_vec_kernel<T, KMAX, ADJ>), grid, dim3(256), 0, st, a);
   } else {
     const int64_t total = a.B * a.H * a.N * a.C;
     hipLaunchKernelGGL((fir_scalar_kernel<T, ADJ>), dim3((total + 255) / 256), dim3(256), 0, st,

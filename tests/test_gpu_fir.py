@@ -4,6 +4,7 @@ import pytest
 import torch
 
 from oracle import pnfirtau_oracle as O
+from paper_01_anti_decoy_pnfirtau_amd import ops  # noqa: F401  (registers torch.ops.pnfx)
 from tests.helpers import bf16_bits, seeded
 
 pytestmark = pytest.mark.gpu

@@ -4,6 +4,7 @@ import pytest
 import torch
 
 from oracle import pnfirtau_oracle as O
+from paper_01_anti_decoy_pnfirtau_amd import ops  # noqa: F401  (registers torch.ops.pnfx)
 from tests.helpers import assert_close, seeded, to_np64
 
 pytestmark = pytest.mark.gpu
