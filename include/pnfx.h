@@ -146,7 +146,7 @@ int pnfx_flash_bwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const v
 /*
  * The three stages of pnfx_flash_bwd, callable separately (same arguments,
  * plus a stage mask): PNFX_BWD_PREPARE forms the per-row constants in the
- * workspace; PNFX_BWD_DKDV writes dk, dv and dtau; PNFX_BWD_DQ writes dq.
+ * workspace; PNFX_BWD_DKDV writes dk and dv; PNFX_BWD_DQ writes dq and dtau.
  * DKDV and DQ each depend only on PREPARE, so a caller may run them on two
  * streams after an event; pnfx_flash_bwd is the mask PNFX_BWD_ALL on one stream.
  */

@@ -29,14 +29,14 @@ struct BwdParams {
   const int32_t* Nmax;
   const uint8_t* mask;
   float* rc;        // row constants [B*H*N][8]: M, r = g/Z, c = 10 g/Z * scale, Dv, G
-  double* partials;  // tau partials [B*H][nkvb][4]
+  double* partials;  // tau partials, one per wave of the dq kernel (bf16: [B*H][N/128][4])
   float* dtau;
   int B, H, N, nq32, nk64, nkvb;
   const float* tau;
   float scale, gamma;
 };
 
-// Key blocks of the key-parallel backward kernel (also sizes the tau partials).
+// Key blocks of the key-parallel backward kernel; 4 * nkvb also bounds the tau partials.
 inline int bwd_nkvb(int64_t N, int64_t D) {
   const int64_t bnk = D <= 64 ? 128 : 64;
   return (int)((N + bnk - 1) / bnk);

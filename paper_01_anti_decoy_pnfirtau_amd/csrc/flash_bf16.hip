@@ -18,10 +18,12 @@
 // the backward therefore sees the forward's ties.
 //
 // Backward (deterministic, no atomics): a per-row preprocess kernel forms the row
-// constants (D_i = <dO_i, O_i>/g_i and the gate/normaliser factors); a query-parallel
-// kernel accumulates dQ; a key-parallel kernel accumulates dK, dV and the tau partials;
-// a one-block kernel sums the partials in fp64.  Both backward kernels skip the 32x64
+// constants (D_i = <dO_i, O_i>/g_i and the gate/normaliser factors); a key-parallel
+// kernel accumulates dK and dV; a query-parallel kernel accumulates dQ and the tau
+// partials; a one-block kernel sums the partials in fp64.  Both backward kernels skip the 32x64
 // sub-tiles that the forward recorded as silent.
+#include <cmath>
+
 #include "flash.h"
 
 namespace pnfx {
@@ -160,6 +162,22 @@ __device__ __forceinline__ void zero_pad_cols(bf16* dst, int tid) {
   }
 }
 
+// Multiply the 8 bf16 values of a fragment by an exact power of two (no rounding).
+__device__ __forceinline__ bf16x8 scale_frag(bf16x8 v, float s) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (bf16)((float)v[e] * s);
+  return v;
+}
+
+// max(x, 0) of an MFMA result in one VALU op.  fmaxf would first canonicalize the operand
+// (an extra op per element: the compiler cannot prove an MFMA accumulator free of
+// signalling NaNs).  On the bit pattern, every negative float (and -0) is a negative
+// int32, so a signed integer max with 0 is relu.  (Not inline asm: the compiler does not
+// insert the MFMA-result wait states in front of an asm statement.)
+__device__ __forceinline__ float relu_mfma(float x) {
+  return __builtin_bit_cast(float, max(__builtin_bit_cast(int, x), 0));
+}
+
 __device__ __forceinline__ float pow10f_(float u) {
   const float u2 = u * u;
   const float u4 = u2 * u2;
@@ -183,7 +201,9 @@ __device__ __forceinline__ void map_block(int nblk, int BH, bool heavy_last_inde
 // s -> u = relu(fma(s, scale, -tau)) in place for the 16 scores a lane holds in one 32-key
 // half tile (S^T layout: key blocks 2*hf, 2*hf+1 x 2 query blocks x 4), zeroing keys past
 // the causal diagonal or N when MASK; returns the lane's per-query-row maximum in tm.
-template <bool MASK>
+// PS: the score scale is a power of two folded into the register-resident operand and -tau
+// into the MFMA accumulator, so s already holds q.k*scale - tau.
+template <bool MASK, bool PS>
 __device__ __forceinline__ void rectify_kq(f32x4 (&s)[2][2], float (&tm)[2], float scale, float ntau,
                                            int n0, int hf, int qrow0, int N, bool causal, int g,
                                            int r16) {
@@ -194,7 +214,7 @@ __device__ __forceinline__ void rectify_kq(f32x4 (&s)[2][2], float (&tm)[2], flo
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float u = fmaxf(__builtin_fmaf(s[kk][qb][i], scale, ntau), 0.f);
+        float u = PS ? relu_mfma(s[kk][qb][i]) : fmaxf(__builtin_fmaf(s[kk][qb][i], scale, ntau), 0.f);
         if (MASK) {
           const int key = n0 + perm_row(2 * hf + kk, 4 * g + i);
           const int qrow = qrow0 + 16 * qb + r16;
@@ -207,8 +227,8 @@ __device__ __forceinline__ void rectify_kq(f32x4 (&s)[2][2], float (&tm)[2], flo
   }
 }
 
-template <int D, bool CAUSAL, bool HAS_GAMMA>
-__global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
+template <int D, bool CAUSAL, bool HAS_GAMMA, bool PS>
+__global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdParams p) {
   constexpr int BM = 128, BN = 64;
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
@@ -240,8 +260,10 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
     for (int ks = 0; ks < KS; ++ks) {
       const int col = 32 * ks + 8 * g;
       qf[qb][ks] = (row < N && col < D) ? ld16(Q + (int64_t)row * p.qsn + col) : zero_bf16x8();
+      if (PS) qf[qb][ks] = scale_frag(qf[qb][ks], scale);
     }
   }
+  const f32x4 s_init = PS ? f32x4{ntau, ntau, ntau, ntau} : f32x4{0.f, 0.f, 0.f, 0.f};
 
   f32x4 acc[DB][2];
 #pragma unroll
@@ -302,7 +324,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
           for (int ks = 0; ks < KS; ++ks) kf[ks] = ld16(Kc + rt_frag<DK>(flr, 2 * hf + kk, ks));
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
-            f32x4 a4 = {0.f, 0.f, 0.f, 0.f};
+            f32x4 a4 = s_init;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) a4 = mfma16x16x32(kf[ks], qf[qb][ks], a4);
             s[kk][qb] = a4;
@@ -310,9 +332,9 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FwdParams p) {
         }
         float tm[2];
         if (masked)
-          rectify_kq<true>(s, tm, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+          rectify_kq<true, PS>(s, tm, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
         else
-          rectify_kq<false>(s, tm, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+          rectify_kq<false, PS>(s, tm, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
         if (!__any(fmaxf(tm[0], tm[1]) > 0.f)) continue;  // silent half: skip P and P.V
         active = true;
         bf16x8 pf[2];
@@ -442,7 +464,7 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
 
 // ds = (c u^9)(dW - D) + [u == M] G for the 16 scores of a lane in one 32-key half tile
 // (S^T layout, query row per lane), written over s.  Row constants are the lane's two rows.
-template <bool MASK>
+template <bool MASK, bool PS>
 __device__ __forceinline__ void ds_kq(f32x4 (&s)[2][2], const f32x4 (&dw)[2][2], const float (&rM)[2],
                                       const float (&rc)[2], const float (&rD)[2], const float (&rG)[2],
                                       float scale, float ntau, int n0, int hf, int qrow0, int N,
@@ -453,7 +475,7 @@ __device__ __forceinline__ void ds_kq(f32x4 (&s)[2][2], const f32x4 (&dw)[2][2],
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float u = fmaxf(__builtin_fmaf(s[kk][qb][i], scale, ntau), 0.f);
+        float u = PS ? relu_mfma(s[kk][qb][i]) : fmaxf(__builtin_fmaf(s[kk][qb][i], scale, ntau), 0.f);
         if (MASK) {
           const int key = n0 + perm_row(2 * hf + kk, 4 * g + i);
           const int qrow = qrow0 + 16 * qb + r16;
@@ -469,7 +491,7 @@ __device__ __forceinline__ void ds_kq(f32x4 (&s)[2][2], const f32x4 (&dw)[2][2],
 
 // dQ: query-parallel, same tiling as the forward (4 waves x 32 rows, 64-key tiles), K and V
 // tiles software-pipelined through LDS (double-buffered when it fits).
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   constexpr int BM = 128, BN = 64;
   constexpr int DK = D < 32 ? 32 : D;
@@ -480,7 +502,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(16))) bf16 Vs[NBUF][BN * DK];
   __shared__ __attribute__((aligned(16))) bf16 Kt[NBUF][D * BN];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
   const int N = p.N;
   const int nqb = (N + BM - 1) / BM;
   int bh, qblk;
@@ -508,6 +531,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       const bool ok = row < N && col < D;
       qf[qb][ks] = ok ? ld16(Q + (int64_t)row * p.qsn + col) : zero_bf16x8();
       dof[qb][ks] = ok ? ld16(dO + (int64_t)row * p.dosn + col) : zero_bf16x8();
+      if (PS) qf[qb][ks] = scale_frag(qf[qb][ks], scale);
     }
     f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
     if (row < N) {
@@ -520,6 +544,15 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
     rG[qb] = c1[0];
   }
 
+  const f32x4 s_init = PS ? f32x4{ntau, ntau, ntau, ntau} : f32x4{0.f, 0.f, 0.f, 0.f};
+  // Sum of every ds the wave forms, accumulated by the MFMA: a constant A fragment whose
+  // row 0 is all ones turns the ds^T operand into its column sums (lanes g == 0, slot 0).
+  f32x4 adt[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  bf16x8 ones = zero_bf16x8();
+  if (r16 == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = (bf16)1.0f;
+  }
   f32x4 acc[DB][2];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -573,7 +606,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
           }
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
-            f32x4 a4 = {0.f, 0.f, 0.f, 0.f}, c4 = {0.f, 0.f, 0.f, 0.f};
+            f32x4 a4 = s_init, c4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
               a4 = mfma16x16x32(kf[ks], qf[qb][ks], a4);
@@ -584,9 +617,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
           }
         }
         if (masked)
-          ds_kq<true>(s, dw, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+          ds_kq<true, PS>(s, dw, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
         else
-          ds_kq<false>(s, dw, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+          ds_kq<false, PS>(s, dw, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
         bf16x8 pf[2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -598,6 +631,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(ktf, pf[qb], acc[db][qb]);
         }
+        adt[0] = mfma16x16x32(ones, pf[0], adt[0]);
+        adt[1] = mfma16x16x32(ones, pf[1], adt[1]);
       }
     }
     if (pre) {
@@ -623,6 +658,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       }
     }
   }
+  double dsum = wave_sum_d(g == 0 ? (double)adt[0][0] + (double)adt[1][0] : 0.0);
+  if (lane == 0) p.partials[((int64_t)bh * nqb + qblk) * 4 + w] = dsum;
 }
 
 // dK, dV and tau partials: key-parallel.  Each wave owns KPW keys (32 for D <= 64, 16 for
@@ -636,13 +673,11 @@ struct DkdvCfg {
 };
 
 // In the S layout (key per lane, four query rows per 16-row block), for one 32-row half
-// (query blocks 2*hf, 2*hf+1): w = u^10 g/Z written over s and ds written over dw; returns
-// the lane's sum of ds.
-template <bool MASK, int KB>
-__device__ __forceinline__ float w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const f32x4* RCc,
-                                         float scale, float ntau, int m0, int hf, int kw0, int N,
-                                         bool causal, int g, int r16) {
-  float tsum = 0.f;
+// (query blocks 2*hf, 2*hf+1): w = u^10 g/Z written over s and ds written over dw.
+template <bool MASK, int KB, bool PS>
+__device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const f32x4* RCc,
+                                        float scale, float ntau, int m0, int hf, int kw0, int N,
+                                        bool causal, int g, int r16) {
 #pragma unroll
   for (int qq = 0; qq < 2; ++qq) {
 #pragma unroll
@@ -653,7 +688,7 @@ __device__ __forceinline__ float w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], 
       const float rG = RCc[2 * lr + 1][0];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        float u = fmaxf(__builtin_fmaf(s[qq][kb][i], scale, ntau), 0.f);
+        float u = PS ? relu_mfma(s[qq][kb][i]) : fmaxf(__builtin_fmaf(s[qq][kb][i], scale, ntau), 0.f);
         if (MASK) {
           const int qrow = m0 + lr;
           const int key = kw0 + 16 * kb + r16;
@@ -665,16 +700,13 @@ __device__ __forceinline__ float w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], 
         const float u9 = u8 * u;
         s[qq][kb][i] = u8 * u2 * rr;  // w = P g / Z
         const float tie = (u == rM) ? rG : 0.f;
-        const float ds = __builtin_fmaf(rcoef * u9, dw[qq][kb][i] - rD, tie);
-        dw[qq][kb][i] = ds;
-        tsum += ds;
+        dw[qq][kb][i] = __builtin_fmaf(rcoef * u9, dw[qq][kb][i] - rD, tie);
       }
     }
   }
-  return tsum;
 }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   constexpr int KPW = DkdvCfg<D>::KPW, KB = DkdvCfg<D>::KB, BNK = DkdvCfg<D>::BNK;
   constexpr int BMQ = 64;
@@ -688,7 +720,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(16))) bf16 dOt[NBUF][D * BMQ];
   __shared__ __attribute__((aligned(16))) f32x4 RC[NBUF][BMQ * 2];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
   const int N = p.N;
   int bh, kvb;
   map_block(p.nkvb, p.B * p.H, false, bh, kvb);
@@ -715,8 +748,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
       const bool ok = key < N && col < D;
       kf[kb][ks] = ok ? ld16(K + (int64_t)key * p.ksn + col) : zero_bf16x8();
       vf[kb][ks] = ok ? ld16(V + (int64_t)key * p.vsn + col) : zero_bf16x8();
+      if (PS) kf[kb][ks] = scale_frag(kf[kb][ks], scale);
     }
   }
+  const f32x4 s_init = PS ? f32x4{ntau, ntau, ntau, ntau} : f32x4{0.f, 0.f, 0.f, 0.f};
   f32x4 adk[DB][KB], adv[DB][KB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -725,7 +760,6 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
       adk[db][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
       adv[db][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-  double dsum = 0.0;  // sum of ds; per-tile fp32 partials are added in fp64
 
   const int nqt = (N + BMQ - 1) / BMQ;
   const int qt0 = CAUSAL ? kv0 / BMQ : 0;
@@ -778,7 +812,6 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
       const bf16* Qtc = Qt[cur];
       const bf16* dOtc = dOt[cur];
       const bool masked = (CAUSAL && m0 < kw0 + KPW - 1) || m0 + BMQ > N || kw0 + KPW > N;
-      float tsum = 0.f;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         if (CAUSAL && m0 + 32 * hf + 31 < kw0) continue;  // rows of this half precede the keys
@@ -794,7 +827,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
           }
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
-            f32x4 a4 = {0.f, 0.f, 0.f, 0.f}, c4 = {0.f, 0.f, 0.f, 0.f};
+            f32x4 a4 = s_init, c4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
               a4 = mfma16x16x32(qa[ks], kf[kb][ks], a4);
@@ -805,9 +838,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
           }
         }
         if (masked)
-          tsum += w_ds_qk<true, KB>(s, dw, RC[cur], scale, ntau, m0, hf, kw0, N, CAUSAL, g, r16);
+          w_ds_qk<true, KB, PS>(s, dw, RC[cur], scale, ntau, m0, hf, kw0, N, CAUSAL, g, r16);
         else
-          tsum += w_ds_qk<false, KB>(s, dw, RC[cur], scale, ntau, m0, hf, kw0, N, CAUSAL, g, r16);
+          w_ds_qk<false, KB, PS>(s, dw, RC[cur], scale, ntau, m0, hf, kw0, N, CAUSAL, g, r16);
         bf16x8 wf[KB], sf[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
@@ -828,7 +861,6 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
           }
         }
       }
-      dsum += (double)tsum;
     }
     if (pre) {
       if (NBUF == 1) __syncthreads();
@@ -855,36 +887,55 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
       }
     }
   }
-  dsum = wave_sum_d(dsum);
-  if (lane == 0) p.partials[((int64_t)bh * p.nkvb + kvb) * 4 + w] = dsum;
 }
 
-// dtau = -(sum of all ds partials) / scale, summed in fp64 by one block in a fixed order.
-__global__ __launch_bounds__(256) void flash_dtau_kernel(const double* partials, int64_t n,
-                                                         float scale, float* dtau) {
-  __shared__ double red[256];
-  double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < n; i += 256) acc += partials[i];
-  red[threadIdx.x] = acc;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-    __syncthreads();
+// dtau = -(sum of all ds partials) / scale, summed in fp64 by one block in a fixed order
+// (deterministic).  Each thread keeps four independent loads in flight.
+__global__ __launch_bounds__(1024) void flash_dtau_kernel(const double* partials, int64_t n,
+                                                          float scale, float* dtau) {
+  __shared__ double red[16];
+  const int tid = threadIdx.x;
+  double a[4] = {0.0, 0.0, 0.0, 0.0};
+  int64_t i = tid;
+  for (; i + 3 * 1024 < n; i += 4 * 1024) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] += partials[i + u * 1024];
   }
-  if (threadIdx.x == 0) dtau[0] = (float)(-red[0] / (double)scale);
+  for (; i < n; i += 1024) a[0] += partials[i];
+  double acc = wave_sum_d((a[0] + a[1]) + (a[2] + a[3]));
+  if ((tid & 63) == 0) red[tid >> 6] = acc;
+  __syncthreads();
+  if (tid < 64) {
+    acc = wave_sum_d(tid < 16 ? red[tid] : 0.0);
+    if (tid == 0) dtau[0] = (float)(-acc / (double)scale);
+  }
+}
+
+// The score scale folds into the operands exactly when it is a power of two (d = 16, 64).
+// All three kernels must make the same choice: the backward's peak-tie test u == M
+// compares its recomputed scores with the forward's M bit for bit.
+bool pow2_scale(float s) {
+  int e;
+  return s > 0.f && std::frexp(s, &e) == 0.5f;
+}
+
+template <int D, bool PS>
+void launch_fwd_dp(const FwdParams& fp, bool causal, bool has_gamma, hipStream_t st) {
+  const int nqb = (fp.N + 127) / 128;
+  const dim3 grid((unsigned)(nqb * fp.B * fp.H)), block(256);
+  if (causal) {
+    if (has_gamma) hipLaunchKernelGGL((flash_fwd_kernel<D, true, true, PS>), grid, block, 0, st, fp);
+    else hipLaunchKernelGGL((flash_fwd_kernel<D, true, false, PS>), grid, block, 0, st, fp);
+  } else {
+    if (has_gamma) hipLaunchKernelGGL((flash_fwd_kernel<D, false, true, PS>), grid, block, 0, st, fp);
+    else hipLaunchKernelGGL((flash_fwd_kernel<D, false, false, PS>), grid, block, 0, st, fp);
+  }
 }
 
 template <int D>
 int launch_fwd_d(const FwdParams& fp, bool causal, bool has_gamma, hipStream_t st) {
-  const int nqb = (fp.N + 127) / 128;
-  const dim3 grid((unsigned)(nqb * fp.B * fp.H)), block(256);
-  if (causal) {
-    if (has_gamma) hipLaunchKernelGGL((flash_fwd_kernel<D, true, true>), grid, block, 0, st, fp);
-    else hipLaunchKernelGGL((flash_fwd_kernel<D, true, false>), grid, block, 0, st, fp);
-  } else {
-    if (has_gamma) hipLaunchKernelGGL((flash_fwd_kernel<D, false, true>), grid, block, 0, st, fp);
-    else hipLaunchKernelGGL((flash_fwd_kernel<D, false, false>), grid, block, 0, st, fp);
-  }
+  if (pow2_scale(fp.scale)) launch_fwd_dp<D, true>(fp, causal, has_gamma, st);
+  else launch_fwd_dp<D, false>(fp, causal, has_gamma, st);
   return launch_status("pnfx_flash_fwd");
 }
 
@@ -900,20 +951,31 @@ int launch_bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, h
     const int rc = launch_status("pnfx_flash_bwd(prepare)");
     if (rc) return rc;
   }
+  const bool ps = pow2_scale(bp.scale);
   if (stages & PNFX_BWD_DKDV) {
     const dim3 gkv((unsigned)(bp.nkvb * bp.B * bp.H));
-    if (causal) hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, true>), gkv, block, 0, st, bp);
-    else hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, false>), gkv, block, 0, st, bp);
-    hipLaunchKernelGGL(flash_dtau_kernel, dim3(1), block, 0, st, bp.partials,
-                       (int64_t)bp.B * bp.H * bp.nkvb * 4, bp.scale, bp.dtau);
+    if (causal) {
+      if (ps) hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, true, true>), gkv, block, 0, st, bp);
+      else hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, true, false>), gkv, block, 0, st, bp);
+    } else {
+      if (ps) hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, false, true>), gkv, block, 0, st, bp);
+      else hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, false, false>), gkv, block, 0, st, bp);
+    }
     const int rc = launch_status("pnfx_flash_bwd(dkdv)");
     if (rc) return rc;
   }
   if (stages & PNFX_BWD_DQ) {
     const int nqb = (bp.N + 127) / 128;
     const dim3 gdq((unsigned)(nqb * bp.B * bp.H));
-    if (causal) hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true>), gdq, block, 0, st, bp);
-    else hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false>), gdq, block, 0, st, bp);
+    if (causal) {
+      if (ps) hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true, true>), gdq, block, 0, st, bp);
+      else hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true, false>), gdq, block, 0, st, bp);
+    } else {
+      if (ps) hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false, true>), gdq, block, 0, st, bp);
+      else hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false, false>), gdq, block, 0, st, bp);
+    }
+    hipLaunchKernelGGL(flash_dtau_kernel, dim3(1), dim3(1024), 0, st, bp.partials,
+                       (int64_t)bp.B * bp.H * nqb * 4, bp.scale, bp.dtau);
     const int rc = launch_status("pnfx_flash_bwd(dq)");
     if (rc) return rc;
   }

@@ -149,6 +149,7 @@ __global__ __launch_bounds__(64) void f32_bwd_dq_kernel(BwdParams p) {
   const int kv_end = CAUSAL ? min((int)(blockIdx.x + 1) * TB, N) : N;
   const int ntiles = (kv_end + TB - 1) / TB;
   const int grp = row >> 5;
+  double dsum = 0.0;  // this row's sum of ds; per-tile fp32 sums are added in fp64
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = t * TB;
     __syncthreads();
@@ -158,6 +159,7 @@ __global__ __launch_bounds__(64) void f32_bwd_dq_kernel(BwdParams p) {
     if (!has) continue;
     if (p.mask && p.mask[((int64_t)bh * p.nq32 + grp) * p.nk64 + t] == 0) continue;
     const int jmax = min(TB, N - n0);
+    float tsum = 0.f;
     for (int j = 0; j < jmax; ++j) {
       if (CAUSAL && n0 + j > row) break;
       float s = 0.f, dw = 0.f;
@@ -172,10 +174,14 @@ __global__ __launch_bounds__(64) void f32_bwd_dq_kernel(BwdParams p) {
       const float u9 = u4 * u4 * u;
       float ds = rcoef * u9 * (dw - rD);
       if (u == rM && u > 0.f) ds += rG;
+      tsum += ds;
 #pragma unroll
       for (int d = 0; d < D; ++d) dq[d] = __builtin_fmaf(ds, Ks[j][d], dq[d]);
     }
+    dsum += (double)tsum;
   }
+  dsum = wave_sum_d(dsum);
+  if (lane == 0) p.partials[(int64_t)bh * gridDim.x + blockIdx.x] = dsum;
   if (!has) return;
   float* dQ = static_cast<float*>(p.dq) + b * p.dqsb + h * p.dqsh + (int64_t)row * p.dqsn;
 #pragma unroll
@@ -202,7 +208,6 @@ __global__ __launch_bounds__(64) void f32_bwd_dkdv_kernel(BwdParams p) {
     dk[d] = 0.f;
     dv[d] = 0.f;
   }
-  double dsum = 0.0;
   const int nqt = (N + TB - 1) / TB;
   const int qt0 = CAUSAL ? blockIdx.x : 0;
   for (int qt = qt0; qt < nqt; ++qt) {
@@ -223,7 +228,6 @@ __global__ __launch_bounds__(64) void f32_bwd_dkdv_kernel(BwdParams p) {
     }
     if (!has) continue;
     const int imax = min(TB, N - m0);
-    float tsum = 0.f;
     for (int i = 0; i < imax; ++i) {
       if (CAUSAL && m0 + i < key) continue;
       float s = 0.f, dw = 0.f;
@@ -238,17 +242,13 @@ __global__ __launch_bounds__(64) void f32_bwd_dkdv_kernel(BwdParams p) {
       const float w = u8 * u2 * RC[i][1];
       float ds = RC[i][2] * (u8 * u) * (dw - RC[i][3]);
       if (u == RC[i][0] && u > 0.f) ds += RC[i][4];
-      tsum += ds;
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         dv[d] = __builtin_fmaf(w, dOs[i][d], dv[d]);
         dk[d] = __builtin_fmaf(ds, Qs[i][d], dk[d]);
       }
     }
-    dsum += (double)tsum;
   }
-  dsum = wave_sum_d(dsum);
-  if (lane == 0) p.partials[(int64_t)bh * gridDim.x + blockIdx.x] = dsum;
   if (!has) return;
   float* dK = static_cast<float*>(p.dk) + b * p.dksb + h * p.dksh + (int64_t)key * p.dksn;
   float* dV = static_cast<float*>(p.dv) + b * p.dvsb + h * p.dvsh + (int64_t)key * p.dvsn;
@@ -301,14 +301,14 @@ int bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, hipStrea
   if (stages & PNFX_BWD_DKDV) {
     if (causal) hipLaunchKernelGGL((f32_bwd_dkdv_kernel<D, true>), grid, block, 0, st, bp);
     else hipLaunchKernelGGL((f32_bwd_dkdv_kernel<D, false>), grid, block, 0, st, bp);
-    hipLaunchKernelGGL(f32_dtau_kernel, dim3(1), dim3(256), 0, st, bp.partials,
-                       (int64_t)bp.B * bp.H * nb, bp.scale, bp.dtau);
     const int rc = launch_status("pnfx_flash_bwd(f32 dkdv)");
     if (rc) return rc;
   }
   if (stages & PNFX_BWD_DQ) {
     if (causal) hipLaunchKernelGGL((f32_bwd_dq_kernel<D, true>), grid, block, 0, st, bp);
     else hipLaunchKernelGGL((f32_bwd_dq_kernel<D, false>), grid, block, 0, st, bp);
+    hipLaunchKernelGGL(f32_dtau_kernel, dim3(1), dim3(256), 0, st, bp.partials,
+                       (int64_t)bp.B * bp.H * nb, bp.scale, bp.dtau);
     const int rc = launch_status("pnfx_flash_bwd(f32 dq)");
     if (rc) return rc;
   }

@@ -67,8 +67,30 @@ def test_flash_matches_oracle(dev, dtype, B, H, N, D, tau, gamma, causal):
     assert_sum_close(float(dtau), rdt, dabs, tol, "dtau")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_flash_stats_and_planted_ties(dev, dtype):
+# bf16 kernels fold a power-of-two scale into the operands and -tau into the MFMA
+# accumulator; any other scale takes the fused multiply-add path.  Both must agree with
+# the oracle, at every head size.
+SCALE_CASES = [(16, 0.1), (32, 0.25), (64, 0.1), (64, 0.5), (128, 0.0625)]
+
+
+@pytest.mark.parametrize("D,scale", SCALE_CASES)
+def test_flash_scale_paths(dev, D, scale):
+    print(f"[flash scale path D={D} scale={scale}]", flush=True)
+    B, H, N = 1, 2, 150
+    q = seeded((B, H, N, D), 24, torch.bfloat16, dev)
+    k = seeded((B, H, N, D), 25, torch.bfloat16, dev)
+    v = seeded((B, H, N, D), 26, torch.bfloat16, dev)
+    dO = seeded((B, H, N, D), 27, torch.bfloat16, dev)
+    o, dq, dk, dv, dtau = _run(q, k, v, 0.1, dO, scale, 0.5, True)
+    Of, M, Z, Nm, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, 0.1, dO, scale, 0.5, True)
+    for name, got, want in (("O", o, Of), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert_bf16_close(to_np64(got), want, name)
+    assert_sum_close(float(dtau), rdt, dabs, BF16_ATOL, "dtau")
+
+
+@pytest.mark.parametrize("dtype,scale", [(torch.bfloat16, 1 / 8), (torch.bfloat16, 0.1),
+                                         (torch.float32, 1 / 8)])
+def test_flash_stats_and_planted_ties(dev, dtype, scale):
     """Duplicate keys give exact score ties at the row peak: Nmax and the gate gradient split."""
     B, H, N, D = 1, 2, 192, 64
     q = seeded((B, H, N, D), 30, dtype, dev)
@@ -78,12 +100,13 @@ def test_flash_stats_and_planted_ties(dev, dtype):
     q[:, :, 160:] = k[:, :, 40:41] * 2.0  # these rows peak on the triplicated key
     v = seeded((B, H, N, D), 32, dtype, dev)
     dO = seeded((B, H, N, D), 33, dtype, dev)
-    o, M, Z, Nm, mask = flash_pn_fir_tau_attention_with_stats(q, k, v, torch.tensor(0.0, device=dev))
-    Of, Mo, Zo, No, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, 0.0, dO, 1 / 8, 0.5, True)
+    o, M, Z, Nm, mask = flash_pn_fir_tau_attention_with_stats(q, k, v, torch.tensor(0.0, device=dev),
+                                                              scale=scale)
+    Of, Mo, Zo, No, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, 0.0, dO, scale, 0.5, True)
     assert (No[:, :, 160:] == 3).all()
     assert np.array_equal(Nm.cpu().numpy()[:, :, 160:], No[:, :, 160:])
     np.testing.assert_allclose(M.cpu().numpy(), Mo, rtol=1e-2 if dtype == torch.bfloat16 else 1e-5)
-    _, dq, dk, dv, dtau = _run(q, k, v, 0.0, dO, 1 / 8, 0.5, True)
+    _, dq, dk, dv, dtau = _run(q, k, v, 0.0, dO, scale, 0.5, True)
     for name, got, want in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
         if dtype == torch.bfloat16:
             assert_bf16_close(to_np64(got), want, name)
