@@ -211,6 +211,27 @@ def bench_copy(dev, mib=512, reps=20):
     return {"copy_bytes_each_way": mib << 20, "reps": reps}
 
 
+def profiled_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.
+
+    The counters need their own profiler passes (profiles/flash_c4_hbm_traffic.md gives the
+    commands and the copy calibration), so the figure is read from that summary rather than
+    measured in this process; None if the summary is absent or names no such kernel.
+    """
+    path = os.path.join(ROOT, "profiles", "flash_c4_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    table = json.loads(line.split(":", 1)[1])
+                    for name, nbytes in table.items():
+                        if name.split("<")[0] == kernel:
+                            return int(nbytes)
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def cpu_baseline(slices=8):
     """numpy oracle (float32) forward + backward on `slices` (b, h) slices of C4."""
     import numpy as np
@@ -307,7 +328,8 @@ def main():
         "event_ms_per_step": round(ev_ms, 4),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved,
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": profiled_traffic(dom),
+                     "traffic_source": "profiles/flash_c4_hbm_traffic.md"},
         "kernels": kern,
         "silent_50": {"silent_fraction": round(frac, 4), "tau": 0.25,
                       "ms_per_step": round(wall_s, 4), "event_ms_per_step": round(ev_s, 4),
