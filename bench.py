@@ -101,7 +101,7 @@ def kernel_times(q, k, v, dO, tau_val, iters):
     B, H, N, D = q.shape
     tau = torch.tensor(tau_val, device=q.device)
     scale, gamma = 1.0 / math.sqrt(D), 0.5
-    o, o_lo, M, Z, Nm, mask = ops.flash_fwd(q, k, v, tau, scale, gamma, True, True, False)
+    o, o_lo, M, Z, _, mask = ops.flash_fwd(q, k, v, tau, scale, gamma, True, True, False, False)
     dq, dk, dv = (torch.empty_like(q) for _ in range(3))
     dtau = torch.empty(1, device=q.device)
     wsb = L.pnfx_flash_bwd_workspace_size(B, H, N, D)
@@ -112,16 +112,17 @@ def kernel_times(q, k, v, dO, tau_val, iters):
     def bwd(stages):
         rc = L.pnfx_flash_bwd_stages(
             stages, *ops._ptr4(q), *ops._ptr4(k), *ops._ptr4(v), *ops._ptr4(o), o_lo.data_ptr(),
-            *ops._ptr4(dO), M.data_ptr(), Z.data_ptr(), Nm.data_ptr(), mask.data_ptr(),
+            *ops._ptr4(dO), M.data_ptr(), Z.data_ptr(), mask.data_ptr(),
             *ops._ptr4(dq), *ops._ptr4(dk), *ops._ptr4(dv), dtau.data_ptr(), ws.data_ptr(), wsb,
             B, H, N, D, t32.data_ptr(), scale, gamma, 1, 1, _lib.PNFX_BF16, st)
         _lib.check(rc, "pnfx_flash_bwd_stages")
 
     stages = {
-        "flash_fwd_kernel": lambda: ops.flash_fwd(q, k, v, tau, scale, gamma, True, True, False),
+        "flash_fwd_kernel": lambda: ops.flash_fwd(q, k, v, tau, scale, gamma, True, True, False,
+                                                  False),
         "flash_bwd_pre_kernel": lambda: bwd(_lib.PNFX_BWD_PREPARE),
-        "flash_bwd_dkdv_kernel": lambda: bwd(_lib.PNFX_BWD_DKDV),
         "flash_bwd_dq_kernel": lambda: bwd(_lib.PNFX_BWD_DQ),
+        "flash_bwd_dkdv_kernel": lambda: bwd(_lib.PNFX_BWD_DKDV),
     }
     gf = gemm_flops(B, H, N, D)
     alg = {"flash_fwd_kernel": 2 * gf, "flash_bwd_pre_kernel": 0,

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define PNFX_ABI_VERSION 1
+#define PNFX_ABI_VERSION 2
 
 #define PNFX_OK 0
 #define PNFX_EINVAL (-1)       /* bad shape / stride / alignment / argument */
@@ -100,7 +100,11 @@ int pnfx_pn_rows_bwd(const void* dw, int64_t dw_rs, const void* raw, int64_t raw
  *   o_lo       : optional (may be NULL; bf16 only), o's strides: the bf16 rounding
  *                residual of O (fp32 O = o + o_lo to ~16 mantissa bits), which
  *                pnfx_flash_bwd uses to form D = <dO, O>/gate accurately
- *   M, Z       : fp32 [B, H, N] contiguous; Nmax: int32 [B, H, N] contiguous
+ *   M, Z       : fp32 [B, H, N] contiguous
+ *   Nmax       : optional (may be NULL) int32 [B, H, N]: the number of keys tied
+ *                at the peak (0 on silent rows).  Counting costs two VALU ops per
+ *                score, so pass NULL unless the counts themselves are wanted: the
+ *                backward does not need them (it counts ties in its dQ stage).
  *   tile_mask  : optional (may be NULL) uint8 [B*H, ceil(N/32), ceil(N/64)]:
  *                1 where the 32-query x 64-key sub-tile has a positive
  *                rectified score (the skip rule of src/triton_pnfirtau.py:395-400
@@ -120,7 +124,7 @@ int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const v
 int64_t pnfx_flash_bwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D);
 
 /*
- * Flash backward.  Inputs as saved by the forward (q, k, v, o, o_lo, M, Z, Nmax,
+ * Flash backward.  Inputs as saved by the forward (q, k, v, o, o_lo, M, Z,
  * tile_mask -- o_lo and tile_mask may be NULL; without tile_mask every causal
  * tile is recomputed),
  * dO with its own strides.  Outputs dq, dk, dv ([B,H,N,D] with their own
@@ -135,7 +139,7 @@ int pnfx_flash_bwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const v
                    int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
                    int64_t vsh, int64_t vsn, const void* o, int64_t osb, int64_t osh,
                    int64_t osn, const void* o_lo, const void* dout, int64_t dosb, int64_t dosh, int64_t dosn,
-                   const float* M, const float* Z, const int32_t* Nmax,
+                   const float* M, const float* Z,
                    const uint8_t* tile_mask, void* dq, int64_t dqsb, int64_t dqsh,
                    int64_t dqsn, void* dk, int64_t dksb, int64_t dksh, int64_t dksn, void* dv,
                    int64_t dvsb, int64_t dvsh, int64_t dvsn, float* dtau, void* workspace,
@@ -145,10 +149,11 @@ int pnfx_flash_bwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const v
 
 /*
  * The three stages of pnfx_flash_bwd, callable separately (same arguments,
- * plus a stage mask): PNFX_BWD_PREPARE forms the per-row constants in the
- * workspace; PNFX_BWD_DKDV writes dk and dv; PNFX_BWD_DQ writes dq and dtau.
- * DKDV and DQ each depend only on PREPARE, so a caller may run them on two
- * streams after an event; pnfx_flash_bwd is the mask PNFX_BWD_ALL on one stream.
+ * plus a stage mask), and run in this order: PNFX_BWD_PREPARE forms the
+ * per-row constants in the workspace; PNFX_BWD_DQ writes dq and dtau and
+ * stores each row's peak-tie share G/Nmax in the workspace; PNFX_BWD_DKDV
+ * (which reads those shares) writes dk and dv.  pnfx_flash_bwd is the mask
+ * PNFX_BWD_ALL.
  */
 #define PNFX_BWD_PREPARE 1
 #define PNFX_BWD_DKDV 2
@@ -159,7 +164,7 @@ int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int64_t qsh, i
                           int64_t vsb, int64_t vsh, int64_t vsn, const void* o, int64_t osb,
                           int64_t osh, int64_t osn, const void* o_lo, const void* dout,
                           int64_t dosb, int64_t dosh, int64_t dosn, const float* M,
-                          const float* Z, const int32_t* Nmax, const uint8_t* tile_mask,
+                          const float* Z, const uint8_t* tile_mask,
                           void* dq, int64_t dqsb, int64_t dqsh, int64_t dqsn, void* dk,
                           int64_t dksb, int64_t dksh, int64_t dksn, void* dv, int64_t dvsb,
                           int64_t dvsh, int64_t dvsn, float* dtau, void* workspace,

@@ -11,6 +11,7 @@ import os
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpnfx.so")
 
+ABI_VERSION = 2
 PNFX_F32 = 0
 PNFX_BF16 = 1
 PNFX_BWD_PREPARE, PNFX_BWD_DKDV, PNFX_BWD_DQ, PNFX_BWD_ALL = 1, 2, 4, 7
@@ -42,7 +43,7 @@ def _declare(lib: ctypes.CDLL) -> None:
             [vp, i64, i64, i64] * 4
             + [vp]
             + [vp, i64, i64, i64]
-            + [vp, vp, vp, vp]
+            + [vp, vp, vp]
             + [vp, i64, i64, i64] * 3
             + [vp, vp, i64, i64, i64, i64, i64, vp, f32, f32, i32, i32, i32, vp], i32),
     }
@@ -63,7 +64,7 @@ def lib() -> ctypes.CDLL:
             )
         handle = ctypes.CDLL(LIB_PATH)
         _declare(handle)
-        if handle.pnfx_abi_version() != 1:
+        if handle.pnfx_abi_version() != ABI_VERSION:
             raise PnfxError("libpnfx.so ABI version mismatch")
         _lib = handle
     return _lib

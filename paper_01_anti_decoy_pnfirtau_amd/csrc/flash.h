@@ -12,11 +12,12 @@ struct FwdParams {
   int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn;
   float* M;
   float* Z;
-  int32_t* Nmax;
+  int32_t* Nmax;  // optional: the peak-tie counts are only formed when requested
   uint8_t* mask;
   int B, H, N, nq32, nk64;
   const float* tau;
   float scale, gamma;
+  int has_gamma;
 };
 
 struct BwdParams {
@@ -26,24 +27,37 @@ struct BwdParams {
   int64_t dqsb, dqsh, dqsn, dksb, dksh, dksn, dvsb, dvsh, dvsn;
   const float* M;
   const float* Z;
-  const int32_t* Nmax;
   const uint8_t* mask;
-  float* rc;        // row constants [B*H*N][8]: M, r = g/Z, c = 10 g/Z * scale, Dv, G
+  float* rc;         // row constants [B*H*N][8]: M, r = g/Z, c = 10 g/Z * scale, Dv, G
   double* partials;  // tau partials, one per wave of the dq kernel (bf16: [B*H][N/128][4])
+  int* flags;        // per dq wave: some row has two or more peak ties
   float* dtau;
   int B, H, N, nq32, nk64, nkvb;
   const float* tau;
   float scale, gamma;
 };
 
-// Key blocks of the key-parallel backward kernel; 4 * nkvb also bounds the tau partials.
+// Key blocks of the key-parallel backward kernel.
 inline int bwd_nkvb(int64_t N, int64_t D) {
   const int64_t bnk = D <= 64 ? 128 : 64;
   return (int)((N + bnk - 1) / bnk);
 }
-int64_t bwd_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D);
+// Workspace of the backward: row constants, then tau partials (fp64) and tie flags (int32),
+// each sized for one entry per 32 query rows (the bf16 dq kernel's waves; the fp32 kernels
+// use one per 64 rows).
+struct BwdWorkspace {
+  int64_t rc_bytes, parts_bytes, flags_bytes;
+  BwdWorkspace(int64_t B, int64_t H, int64_t N) {
+    const int64_t slots = B * H * ((N + 127) / 128) * 4;
+    rc_bytes = round256(B * H * N * 8 * 4);
+    parts_bytes = round256(slots * 8);
+    flags_bytes = round256(slots * 4);
+  }
+  int64_t total() const { return rc_bytes + parts_bytes + flags_bytes; }
+  static int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
+};
 
-int flash_fwd_bf16(const FwdParams& fp, int64_t D, bool causal, bool has_gamma, hipStream_t st);
+int flash_fwd_bf16(const FwdParams& fp, int64_t D, bool causal, hipStream_t st);
 int flash_bwd_bf16(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, int stages,
                    hipStream_t st);
 int flash_fwd_f32(const FwdParams& fp, int64_t D, bool causal, bool has_gamma, hipStream_t st);

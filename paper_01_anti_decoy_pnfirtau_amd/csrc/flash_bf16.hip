@@ -227,7 +227,8 @@ __device__ __forceinline__ void rectify_kq(f32x4 (&s)[2][2], float (&tm)[2], flo
   }
 }
 
-template <int D, bool CAUSAL, bool HAS_GAMMA, bool PS>
+// COUNT: also count the peak ties (Nmax); the training path leaves that to the backward.
+template <int D, bool CAUSAL, bool PS, bool COUNT>
 __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdParams p) {
   constexpr int BM = 128, BN = 64;
   constexpr int DK = D < 32 ? 32 : D;
@@ -236,7 +237,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][BN * DK];
   __shared__ __attribute__((aligned(16))) bf16 Vt[2][D * BN];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
   const int N = p.N;
   const int nqb = (N + BM - 1) / BM;
   int bh, qblk;
@@ -341,12 +343,14 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
           const float mnew = fmaxf(mrun[qb], tm[qb]);
-          int c = (mnew == mrun[qb]) ? cnt[qb] : 0;
+          if (COUNT) {
+            int c = (mnew == mrun[qb]) ? cnt[qb] : 0;
 #pragma unroll
-          for (int kk = 0; kk < 2; ++kk)
+            for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) c += (s[kk][qb][i] == mnew) ? 1 : 0;
-          cnt[qb] = c;
+              for (int i = 0; i < 4; ++i) c += (s[kk][qb][i] == mnew) ? 1 : 0;
+            cnt[qb] = c;
+          }
           mrun[qb] = mnew;
           pf[qb] = pack8(pow10f_(s[0][qb][0]), pow10f_(s[0][qb][1]), pow10f_(s[0][qb][2]),
                          pow10f_(s[0][qb][3]), pow10f_(s[1][qb][0]), pow10f_(s[1][qb][1]),
@@ -380,12 +384,15 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
     const float m = mrun[qb];
     float Mx = fmaxf(m, __shfl_xor(m, 16, 64));
     Mx = fmaxf(Mx, __shfl_xor(Mx, 32, 64));
-    int c = (m == Mx) ? cnt[qb] : 0;
-    c += __shfl_xor(c, 16, 64);
-    c += __shfl_xor(c, 32, 64);
+    int c = 0;
+    if (COUNT) {
+      c = (m == Mx) ? cnt[qb] : 0;
+      c += __shfl_xor(c, 16, 64);
+      c += __shfl_xor(c, 32, 64);
+    }
     // row 0 of the mass block lives in lane r16 (lane group 0), register 0
     const float ms = __shfl(accm[qb][0], r16, 64);
-    const float gate = Mx > 0.f ? (HAS_GAMMA ? Mx / (Mx + p.gamma) : 1.f) : 0.f;
+    const float gate = Mx > 0.f ? (p.has_gamma ? Mx / (Mx + p.gamma) : 1.f) : 0.f;
     const float z = ms + 1e-12f;
     const float so = gate / z;
     const int qrow = qrow0 + 16 * qb + r16;
@@ -407,7 +414,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
         const int64_t si = (int64_t)bh * N + qrow;
         p.M[si] = Mx;
         p.Z[si] = z;
-        p.Nmax[si] = Mx > 0.f ? c : 0;
+        if (COUNT) p.Nmax[si] = Mx > 0.f ? c : 0;
       }
     }
   }
@@ -415,7 +422,10 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
 
 // ------------------------------------------------------------------------------ backward
 // Row constants: D_i = <dO_i, O_i> / g_i (the flash identity of src/triton_pnfirtau.py:575-577),
-// r = g/Z, c = 10 g/Z * scale, G = D gamma/(M+gamma)^2 / Nmax * scale (zero on silent rows).
+// r = g/Z, c = 10 g/Z * scale, and G = D gamma/(M+gamma)^2 * scale, the gradient of the
+// gate through the peak for the whole row (zero on silent rows and without a gate).  The
+// Nmax keys tied at the peak share it, G/Nmax each (src/triton_pnfirtau.py:580-586); the
+// dQ kernel counts the ties and stores G/Nmax in place of G for the dK/dV kernel.
 template <int D, bool HAS_GAMMA>
 __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   constexpr int LPR = D / 8;  // lanes per row
@@ -453,7 +463,7 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
     float G = 0.f;
     if (HAS_GAMMA && M > 0.f) {
       const float dgate = p.gamma / ((M + p.gamma) * (M + p.gamma));
-      G = Dv * dgate / (float)p.Nmax[row] * p.scale;
+      G = Dv * dgate * p.scale;
     }
     f32x4 c0 = {M, g / Z, 10.f * g / Z * p.scale, Dv};
     f32x4 c1 = {G, 0.f, 0.f, 0.f};
@@ -462,17 +472,19 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   }
 }
 
-// ds = (c u^9)(dW - D) + [u == M] G for the 16 scores of a lane in one 32-key half tile
-// (S^T layout, query row per lane), written over s.  Row constants are the lane's two rows.
-template <bool MASK, bool PS>
-__device__ __forceinline__ void ds_kq(f32x4 (&s)[2][2], const f32x4 (&dw)[2][2], const float (&rM)[2],
-                                      const float (&rc)[2], const float (&rD)[2], const float (&rG)[2],
-                                      float scale, float ntau, int n0, int hf, int qrow0, int N,
-                                      bool causal, int g, int r16) {
+// dS for the 16 scores a lane holds in one 32-key half tile of the dQ kernel (S^T layout,
+// one query row per lane), written over dw: (c u^9)(dW - D) + [u == M] G.  COUNT also
+// counts the peak ties per query block.
+template <bool MASK, bool PS, bool COUNT>
+__device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2], int (&cnt)[2],
+                                      const float (&rM)[2], const float (&rc)[2],
+                                      const float (&rD)[2], const float (&rG)[2], float scale,
+                                      float ntau, int n0, int hf, int qrow0, int N, bool causal,
+                                      int g, int r16) {
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
+  for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float u = PS ? relu_mfma(s[kk][qb][i]) : fmaxf(__builtin_fmaf(s[kk][qb][i], scale, ntau), 0.f);
@@ -484,14 +496,25 @@ __device__ __forceinline__ void ds_kq(f32x4 (&s)[2][2], const f32x4 (&dw)[2][2],
         const float u2 = u * u;
         const float u4 = u2 * u2;
         const float u9 = u4 * u4 * u;
-        const float tie = (u == rM[qb]) ? rG[qb] : 0.f;  // G = 0 on silent rows
-        s[kk][qb][i] = __builtin_fmaf(rc[qb] * u9, dw[kk][qb][i] - rD[qb], tie);
+        const bool tie = u == rM[qb];  // rG = 0 on silent rows
+        dw[kk][qb][i] = __builtin_fmaf(rc[qb] * u9, dw[kk][qb][i] - rD[qb], tie ? rG[qb] : 0.f);
+        if (COUNT) cnt[qb] += tie ? 1 : 0;
       }
 }
 
 // dQ: query-parallel, same tiling as the forward (4 waves x 32 rows, 64-key tiles), K and V
 // tiles software-pipelined through LDS (double-buffered when it fits).
-template <int D, bool CAUSAL, bool PS>
+//
+// Peak ties.  A key tied at the row's peak gets the extra gradient G/Nmax.  The forward
+// does not count ties, so this kernel runs as two passes.  DQ_COUNT: the tie term uses the
+// whole-row G per tied key while the ties are counted (one compare serves both); afterwards
+// G/Nmax replaces G in the row constants (for the dK/dV kernel), the tau partial is
+// corrected to G per row, and each wave flags whether any of its rows had two or more ties.
+// DQ_FIX: only workgroups with a flagged wave run; they recompute dQ with G/Nmax (on
+// typical inputs every row has a single peak and nothing is flagged).
+enum { DQ_COUNT = 0, DQ_FIX = 1 };
+
+template <int D, bool CAUSAL, bool PS, int MODE>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   constexpr int BM = 128, BN = 64;
   constexpr int DK = D < 32 ? 32 : D;
@@ -519,6 +542,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   const float ntau = -p.tau[0];
   const float scale = p.scale;
   const FragLane flr = rt_lane<DK>(r16, g), flt = tt_lane(r16, g);
+  int* const wflag = p.flags + ((int64_t)bh * nqb + qblk) * 4;
+  if (MODE == DQ_FIX && (wflag[0] | wflag[1] | wflag[2] | wflag[3]) == 0) return;  // whole block
 
   bf16x8 qf[2][KS], dof[2][KS];
   float rM[2], rc[2], rD[2], rG[2];
@@ -545,6 +570,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   }
 
   const f32x4 s_init = PS ? f32x4{ntau, ntau, ntau, ntau} : f32x4{0.f, 0.f, 0.f, 0.f};
+  int cnt[2] = {0, 0};  // lane-local tie counts (DQ_COUNT)
   // Sum of every ds the wave forms, accumulated by the MFMA: a constant A fragment whose
   // row 0 is all ones turns the ds^T operand into its column sums (lanes g == 0, slot 0).
   f32x4 adt[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -616,15 +642,18 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
             dw[kk][qb] = c4;
           }
         }
+        constexpr bool COUNT = MODE == DQ_COUNT;
         if (masked)
-          ds_kq<true, PS>(s, dw, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+          ds_kq<true, PS, COUNT>(s, dw, cnt, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N,
+                                 CAUSAL, g, r16);
         else
-          ds_kq<false, PS>(s, dw, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+          ds_kq<false, PS, COUNT>(s, dw, cnt, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N,
+                                  CAUSAL, g, r16);
         bf16x8 pf[2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
-          pf[qb] = pack8(s[0][qb][0], s[0][qb][1], s[0][qb][2], s[0][qb][3], s[1][qb][0],
-                         s[1][qb][1], s[1][qb][2], s[1][qb][3]);
+          pf[qb] = pack8(dw[0][qb][0], dw[0][qb][1], dw[0][qb][2], dw[0][qb][3], dw[1][qb][0],
+                         dw[1][qb][1], dw[1][qb][2], dw[1][qb][3]);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const bf16x8 ktf = ld16(Ktc + tt_frag(flt, db, hf));
@@ -658,8 +687,29 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       }
     }
   }
-  double dsum = wave_sum_d(g == 0 ? (double)adt[0][0] + (double)adt[1][0] : 0.0);
-  if (lane == 0) p.partials[((int64_t)bh * nqb + qblk) * 4 + w] = dsum;
+  if (MODE == DQ_FIX) return;
+  // Tie counts per row (the four lane groups of a row), G -> G/Nmax for the dK/dV kernel,
+  // and the tau partial: the MFMA sum holds Nmax G per row for ties whose gradient is G.
+  double dsum = g == 0 ? (double)adt[0][0] + (double)adt[1][0] : 0.0;
+  bool multi = false;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    int c = cnt[qb];
+    c += __shfl_xor(c, 16, 64);
+    c += __shfl_xor(c, 32, 64);
+    const int qrow = qrow0 + 16 * qb + r16;
+    if (g == 0 && qrow < N) {
+      p.rc[8 * ((int64_t)bh * N + qrow) + 4] = c > 0 ? rG[qb] / (float)c : 0.f;
+      if (c > 1) dsum -= (double)rG[qb] * (double)(c - 1);
+    }
+    multi = multi || (c > 1 && rG[qb] != 0.f);
+  }
+  dsum = wave_sum_d(dsum);
+  multi = __any(multi);
+  if (lane == 0) {
+    p.partials[((int64_t)bh * nqb + qblk) * 4 + w] = dsum;
+    wflag[w] = multi ? 1 : 0;
+  }
 }
 
 // dK, dV and tau partials: key-parallel.  Each wave owns KPW keys (32 for D <= 64, 16 for
@@ -920,23 +970,37 @@ bool pow2_scale(float s) {
 }
 
 template <int D, bool PS>
-void launch_fwd_dp(const FwdParams& fp, bool causal, bool has_gamma, hipStream_t st) {
+void launch_fwd_dp(const FwdParams& fp, bool causal, hipStream_t st) {
   const int nqb = (fp.N + 127) / 128;
   const dim3 grid((unsigned)(nqb * fp.B * fp.H)), block(256);
+  const bool count = fp.Nmax != nullptr;
   if (causal) {
-    if (has_gamma) hipLaunchKernelGGL((flash_fwd_kernel<D, true, true, PS>), grid, block, 0, st, fp);
-    else hipLaunchKernelGGL((flash_fwd_kernel<D, true, false, PS>), grid, block, 0, st, fp);
+    if (count) hipLaunchKernelGGL((flash_fwd_kernel<D, true, PS, true>), grid, block, 0, st, fp);
+    else hipLaunchKernelGGL((flash_fwd_kernel<D, true, PS, false>), grid, block, 0, st, fp);
   } else {
-    if (has_gamma) hipLaunchKernelGGL((flash_fwd_kernel<D, false, true, PS>), grid, block, 0, st, fp);
-    else hipLaunchKernelGGL((flash_fwd_kernel<D, false, false, PS>), grid, block, 0, st, fp);
+    if (count) hipLaunchKernelGGL((flash_fwd_kernel<D, false, PS, true>), grid, block, 0, st, fp);
+    else hipLaunchKernelGGL((flash_fwd_kernel<D, false, PS, false>), grid, block, 0, st, fp);
   }
 }
 
 template <int D>
-int launch_fwd_d(const FwdParams& fp, bool causal, bool has_gamma, hipStream_t st) {
-  if (pow2_scale(fp.scale)) launch_fwd_dp<D, true>(fp, causal, has_gamma, st);
-  else launch_fwd_dp<D, false>(fp, causal, has_gamma, st);
+int launch_fwd_d(const FwdParams& fp, bool causal, hipStream_t st) {
+  if (pow2_scale(fp.scale)) launch_fwd_dp<D, true>(fp, causal, st);
+  else launch_fwd_dp<D, false>(fp, causal, st);
   return launch_status("pnfx_flash_fwd");
+}
+
+// The counting pass, then the fix-up pass (workgroups without a flagged wave exit at once).
+template <int D, bool PS>
+void launch_dq(const BwdParams& bp, bool causal, dim3 grid, hipStream_t st) {
+  const dim3 block(256);
+  if (causal) {
+    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true, PS, DQ_COUNT>), grid, block, 0, st, bp);
+    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true, PS, DQ_FIX>), grid, block, 0, st, bp);
+  } else {
+    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false, PS, DQ_COUNT>), grid, block, 0, st, bp);
+    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false, PS, DQ_FIX>), grid, block, 0, st, bp);
+  }
 }
 
 template <int D>
@@ -952,7 +1016,17 @@ int launch_bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, h
     if (rc) return rc;
   }
   const bool ps = pow2_scale(bp.scale);
-  if (stages & PNFX_BWD_DKDV) {
+  if (stages & PNFX_BWD_DQ) {
+    const int nqb = (bp.N + 127) / 128;
+    const dim3 gdq((unsigned)(nqb * bp.B * bp.H));
+    if (ps) launch_dq<D, true>(bp, causal, gdq, st);
+    else launch_dq<D, false>(bp, causal, gdq, st);
+    hipLaunchKernelGGL(flash_dtau_kernel, dim3(1), dim3(1024), 0, st, bp.partials,
+                       (int64_t)bp.B * bp.H * nqb * 4, bp.scale, bp.dtau);
+    const int rc = launch_status("pnfx_flash_bwd(dq)");
+    if (rc) return rc;
+  }
+  if (stages & PNFX_BWD_DKDV) {  // reads the G/Nmax the dQ stage wrote
     const dim3 gkv((unsigned)(bp.nkvb * bp.B * bp.H));
     if (causal) {
       if (ps) hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, true, true>), gkv, block, 0, st, bp);
@@ -964,38 +1038,19 @@ int launch_bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, h
     const int rc = launch_status("pnfx_flash_bwd(dkdv)");
     if (rc) return rc;
   }
-  if (stages & PNFX_BWD_DQ) {
-    const int nqb = (bp.N + 127) / 128;
-    const dim3 gdq((unsigned)(nqb * bp.B * bp.H));
-    if (causal) {
-      if (ps) hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true, true>), gdq, block, 0, st, bp);
-      else hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true, false>), gdq, block, 0, st, bp);
-    } else {
-      if (ps) hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false, true>), gdq, block, 0, st, bp);
-      else hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false, false>), gdq, block, 0, st, bp);
-    }
-    hipLaunchKernelGGL(flash_dtau_kernel, dim3(1), dim3(1024), 0, st, bp.partials,
-                       (int64_t)bp.B * bp.H * nqb * 4, bp.scale, bp.dtau);
-    const int rc = launch_status("pnfx_flash_bwd(dq)");
-    if (rc) return rc;
-  }
   return PNFX_OK;
 }
 
 }  // namespace
 
-int64_t bwd_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t D) {
-  const int64_t rc = B * H * N * 8 * 4;
-  const int64_t parts = B * H * bwd_nkvb(N, D) * 4 * 8;
-  return ((rc + 255) / 256) * 256 + ((parts + 255) / 256) * 256;
-}
 
-int flash_fwd_bf16(const FwdParams& fp, int64_t D, bool causal, bool has_gamma, hipStream_t st) {
+
+int flash_fwd_bf16(const FwdParams& fp, int64_t D, bool causal, hipStream_t st) {
   switch (D) {
-    case 16: return launch_fwd_d<16>(fp, causal, has_gamma, st);
-    case 32: return launch_fwd_d<32>(fp, causal, has_gamma, st);
-    case 64: return launch_fwd_d<64>(fp, causal, has_gamma, st);
-    case 128: return launch_fwd_d<128>(fp, causal, has_gamma, st);
+    case 16: return launch_fwd_d<16>(fp, causal, st);
+    case 32: return launch_fwd_d<32>(fp, causal, st);
+    case 64: return launch_fwd_d<64>(fp, causal, st);
+    case 128: return launch_fwd_d<128>(fp, causal, st);
   }
   set_error("flash: head dim %lld not in {16, 32, 64, 128}", (long long)D);
   return PNFX_EUNSUPPORTED;

@@ -49,19 +49,20 @@ extern "C" int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t q
   if ((rc = check_operand("k", k, ksb, ksh, ksn, dtype))) return rc;
   if ((rc = check_operand("v", v, vsb, vsh, vsn, dtype))) return rc;
   if ((rc = check_operand("o", o, osb, osh, osn, dtype))) return rc;
-  PNFX_REQUIRE(M && Z && Nmax && tau, "flash_fwd: null statistics / tau pointer");
+  PNFX_REQUIRE(M && Z && tau, "flash_fwd: null statistics / tau pointer");
   PNFX_REQUIRE(!o_lo || (dtype == PNFX_BF16 && aligned16(o_lo)),
                "flash_fwd: o_lo is a 16-byte aligned bf16 buffer with o's strides");
   FwdParams fp{q, k, v, o, o_lo, qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn,
                M, Z, Nmax, tile_mask, (int)B, (int)H, (int)N,
-               (int)((N + 31) / 32), (int)((N + 63) / 64), tau, scale, gamma};
+               (int)((N + 31) / 32), (int)((N + 63) / 64), tau, scale, gamma, has_gamma != 0};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  return dtype == PNFX_BF16 ? flash_fwd_bf16(fp, D, causal != 0, has_gamma != 0, st)
+  return dtype == PNFX_BF16 ? flash_fwd_bf16(fp, D, causal != 0, st)
                             : flash_fwd_f32(fp, D, causal != 0, has_gamma != 0, st);
 }
 
 extern "C" int64_t pnfx_flash_bwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D) {
-  return bwd_workspace_bytes(B, H, N, D);
+  (void)D;
+  return BwdWorkspace(B, H, N).total();
 }
 
 extern "C" int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
@@ -69,7 +70,7 @@ extern "C" int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int
                               int64_t vsh, int64_t vsn, const void* o, int64_t osb, int64_t osh,
                               int64_t osn, const void* o_lo, const void* dout, int64_t dosb,
                               int64_t dosh,
-                              int64_t dosn, const float* M, const float* Z, const int32_t* Nmax,
+                              int64_t dosn, const float* M, const float* Z,
                               const uint8_t* tile_mask, void* dq, int64_t dqsb, int64_t dqsh,
                               int64_t dqsn, void* dk, int64_t dksb, int64_t dksh, int64_t dksn,
                               void* dv, int64_t dvsb, int64_t dvsh, int64_t dvsn, float* dtau,
@@ -88,20 +89,22 @@ extern "C" int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int
   if ((rc = check_operand("dq", dq, dqsb, dqsh, dqsn, dtype))) return rc;
   if ((rc = check_operand("dk", dk, dksb, dksh, dksn, dtype))) return rc;
   if ((rc = check_operand("dv", dv, dvsb, dvsh, dvsn, dtype))) return rc;
-  PNFX_REQUIRE(M && Z && Nmax && tau && dtau, "flash_bwd: null statistics / tau pointer");
+  PNFX_REQUIRE(M && Z && tau && dtau, "flash_bwd: null statistics / tau pointer");
   PNFX_REQUIRE(!o_lo || (dtype == PNFX_BF16 && aligned16(o_lo)),
                "flash_bwd: o_lo is a 16-byte aligned bf16 buffer with o's strides");
-  const int64_t need = bwd_workspace_bytes(B, H, N, D);
-  PNFX_REQUIRE(workspace && workspace_bytes >= need && (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
-               "flash_bwd: workspace needs %lld bytes, 256-byte aligned (got %lld)", (long long)need,
-               (long long)workspace_bytes);
-  const int64_t rc_bytes = ((B * H * N * 8 * 4 + 255) / 256) * 256;
-  float* rcbuf = static_cast<float*>(workspace);
-  double* parts = reinterpret_cast<double*>(static_cast<char*>(workspace) + rc_bytes);
+  const BwdWorkspace wl(B, H, N);
+  PNFX_REQUIRE(workspace && workspace_bytes >= wl.total() &&
+                   (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
+               "flash_bwd: workspace needs %lld bytes, 256-byte aligned (got %lld)",
+               (long long)wl.total(), (long long)workspace_bytes);
+  char* ws = static_cast<char*>(workspace);
+  float* rcbuf = reinterpret_cast<float*>(ws);
+  double* parts = reinterpret_cast<double*>(ws + wl.rc_bytes);
+  int* flags = reinterpret_cast<int*>(ws + wl.rc_bytes + wl.parts_bytes);
   BwdParams bp{q, k, v, o, o_lo, dout, dq, dk, dv,
                qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn, dosb, dosh, dosn,
                dqsb, dqsh, dqsn, dksb, dksh, dksn, dvsb, dvsh, dvsn,
-               M, Z, Nmax, tile_mask, rcbuf, parts, dtau,
+               M, Z, tile_mask, rcbuf, parts, flags, dtau,
                (int)B, (int)H, (int)N, (int)((N + 31) / 32), (int)((N + 63) / 64),
                bwd_nkvb(N, D), tau, scale, gamma};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -114,7 +117,7 @@ extern "C" int pnfx_flash_bwd(const void* q, int64_t qsb, int64_t qsh, int64_t q
                               int64_t vsh, int64_t vsn, const void* o, int64_t osb, int64_t osh,
                               int64_t osn, const void* o_lo, const void* dout, int64_t dosb,
                               int64_t dosh, int64_t dosn, const float* M, const float* Z,
-                              const int32_t* Nmax, const uint8_t* tile_mask, void* dq,
+                              const uint8_t* tile_mask, void* dq,
                               int64_t dqsb, int64_t dqsh, int64_t dqsn, void* dk, int64_t dksb,
                               int64_t dksh, int64_t dksn, void* dv, int64_t dvsb, int64_t dvsh,
                               int64_t dvsn, float* dtau, void* workspace, int64_t workspace_bytes,
@@ -122,7 +125,7 @@ extern "C" int pnfx_flash_bwd(const void* q, int64_t qsb, int64_t qsh, int64_t q
                               float scale, float gamma, int has_gamma, int causal, int dtype,
                               void* stream) {
   return pnfx_flash_bwd_stages(PNFX_BWD_ALL, q, qsb, qsh, qsn, k, ksb, ksh, ksn, v, vsb, vsh, vsn,
-                               o, osb, osh, osn, o_lo, dout, dosb, dosh, dosn, M, Z, Nmax,
+                               o, osb, osh, osn, o_lo, dout, dosb, dosh, dosn, M, Z,
                                tile_mask, dq, dqsb, dqsh, dqsn, dk, dksb, dksh, dksn, dv, dvsb,
                                dvsh, dvsn, dtau, workspace, workspace_bytes, B, H, N, D, tau,
                                scale, gamma, has_gamma, causal, dtype, stream);

@@ -4,7 +4,8 @@
 // tiles of the other operand staged in LDS and read as broadcasts.  Dot products are a
 // sequential fma chain over the head dimension in the same order in every kernel, so the
 // backward reproduces the forward's scores bit for bit (the u == peak tie test relies on
-// it).  Same math, statistics, tile mask and workspace layout as the bf16 MFMA kernels.
+// it).  Same math, statistics, tile mask and workspace layout as the bf16 MFMA kernels; the
+// dQ kernel counts the peak ties itself with one extra sweep of the scores.
 #include "flash.h"
 
 namespace pnfx {
@@ -97,7 +98,7 @@ __global__ __launch_bounds__(64) void f32_fwd_kernel(FwdParams p) {
   const int64_t si = (int64_t)bh * N + row;
   p.M[si] = m;
   p.Z[si] = z;
-  p.Nmax[si] = m > 0.f ? cnt : 0;
+  if (p.Nmax) p.Nmax[si] = m > 0.f ? cnt : 0;
 }
 
 template <int D, bool HAS_GAMMA>
@@ -112,10 +113,10 @@ __global__ __launch_bounds__(256) void f32_bwd_pre_kernel(BwdParams p) {
   const float M = p.M[row], Z = p.Z[row];
   const float g = M > 0.f ? (HAS_GAMMA ? M / (M + p.gamma) : 1.f) : 0.f;
   const float Dv = g > 0.f ? dot / g : 0.f;
-  float G = 0.f;
+  float G = 0.f;  // the whole row's peak-tie gradient; the dQ kernel divides it by Nmax
   if (HAS_GAMMA && M > 0.f) {
     const float dgate = p.gamma / ((M + p.gamma) * (M + p.gamma));
-    G = Dv * dgate / (float)p.Nmax[row] * p.scale;
+    G = Dv * dgate * p.scale;
   }
   float* rc = p.rc + 8 * row;
   rc[0] = M;
@@ -144,10 +145,32 @@ __global__ __launch_bounds__(64) void f32_bwd_dq_kernel(BwdParams p) {
     gdo[d] = has ? dO[(int64_t)row * p.dosn + d] : 0.f;
     dq[d] = 0.f;
   }
-  const float* rcp = p.rc + 8 * ((int64_t)bh * N + (has ? row : 0));
-  const float rM = rcp[0], rcoef = rcp[2], rD = rcp[3], rG = rcp[4];
+  float* rcp = p.rc + 8 * ((int64_t)bh * N + (has ? row : 0));
+  const float rM = rcp[0], rcoef = rcp[2], rD = rcp[3];
   const int kv_end = CAUSAL ? min((int)(blockIdx.x + 1) * TB, N) : N;
   const int ntiles = (kv_end + TB - 1) / TB;
+  // Count the keys tied at the peak (the forward leaves Nmax to the backward): one sweep of
+  // the scores, computed exactly as below, so G/Nmax is known before dQ accumulates.
+  int nmax = 0;
+  for (int t = 0; t < ntiles; ++t) {
+    const int n0 = t * TB;
+    __syncthreads();
+    stage<D>(Ks, K, p.ksn, n0, N);
+    __syncthreads();
+    if (!has || rM <= 0.f) continue;
+    const int jmax = min(TB, N - n0);
+    for (int j = 0; j < jmax; ++j) {
+      if (CAUSAL && n0 + j > row) break;
+      float s = 0.f;
+#pragma unroll
+      for (int d = 0; d < D; ++d) s = __builtin_fmaf(q[d], Ks[j][d], s);
+      const float sv = __builtin_fmaf(s, p.scale, ntau);
+      nmax += (sv > 0.f ? sv : 0.f) == rM ? 1 : 0;
+    }
+  }
+  const float rG = nmax > 0 ? rcp[4] / (float)nmax : 0.f;
+  __syncthreads();
+  if (has) rcp[4] = rG;  // read by the dK/dV kernel
   const int grp = row >> 5;
   double dsum = 0.0;  // this row's sum of ds; per-tile fp32 sums are added in fp64
   for (int t = 0; t < ntiles; ++t) {
@@ -298,18 +321,18 @@ int bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, hipStrea
     const int rc = launch_status("pnfx_flash_bwd(f32 prepare)");
     if (rc) return rc;
   }
-  if (stages & PNFX_BWD_DKDV) {
-    if (causal) hipLaunchKernelGGL((f32_bwd_dkdv_kernel<D, true>), grid, block, 0, st, bp);
-    else hipLaunchKernelGGL((f32_bwd_dkdv_kernel<D, false>), grid, block, 0, st, bp);
-    const int rc = launch_status("pnfx_flash_bwd(f32 dkdv)");
-    if (rc) return rc;
-  }
   if (stages & PNFX_BWD_DQ) {
     if (causal) hipLaunchKernelGGL((f32_bwd_dq_kernel<D, true>), grid, block, 0, st, bp);
     else hipLaunchKernelGGL((f32_bwd_dq_kernel<D, false>), grid, block, 0, st, bp);
     hipLaunchKernelGGL(f32_dtau_kernel, dim3(1), dim3(256), 0, st, bp.partials,
                        (int64_t)bp.B * bp.H * nb, bp.scale, bp.dtau);
     const int rc = launch_status("pnfx_flash_bwd(f32 dq)");
+    if (rc) return rc;
+  }
+  if (stages & PNFX_BWD_DKDV) {  // reads the G/Nmax the dQ stage wrote
+    if (causal) hipLaunchKernelGGL((f32_bwd_dkdv_kernel<D, true>), grid, block, 0, st, bp);
+    else hipLaunchKernelGGL((f32_bwd_dkdv_kernel<D, false>), grid, block, 0, st, bp);
+    const int rc = launch_status("pnfx_flash_bwd(f32 dkdv)");
     if (rc) return rc;
   }
   return PNFX_OK;

@@ -88,7 +88,7 @@ def _flash_attention(q, k, v, score_tau, scale, gamma, causal_mask, o_bnhd=False
     has_gamma = gamma is not None and gamma > 0.0
     o = torch.ops.pnfx.flash_fwd(q, k, v, score_tau, float(scale),
                                  float(gamma) if has_gamma else 0.0, has_gamma,
-                                 bool(causal_mask), bool(o_bnhd))[0]
+                                 bool(causal_mask), bool(o_bnhd), False)[0]
     return o
 
 
@@ -120,7 +120,7 @@ def flash_pn_fir_tau_attention_with_stats(q, k_tilde, v, score_tau, scale=None, 
     has_gamma = gamma is not None and gamma > 0.0
     o, _, M, Z, Nm, mask = torch.ops.pnfx.flash_fwd(q, k_tilde, v, score_tau, float(scale),
                                                    float(gamma) if has_gamma else 0.0, has_gamma,
-                                                   bool(causal_mask), False)
+                                                   bool(causal_mask), False, True)
     return o, M, Z, Nm, mask
 
 

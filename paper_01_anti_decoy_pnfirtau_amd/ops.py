@@ -192,15 +192,16 @@ def _new_o(q: Tensor, o_bnhd: bool) -> Tensor:
 
 @torch.library.custom_op("pnfx::flash_fwd", mutates_args=(), device_types="cuda")
 def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma: float,
-              has_gamma: bool, causal: bool,
-              o_bnhd: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+              has_gamma: bool, causal: bool, o_bnhd: bool,
+              with_nmax: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Flash forward on [B,H,N,D]; returns (O, O_lo, M, Z, Nmax, tile_mask).
 
     O has shape [B,H,N,D]; with o_bnhd it is backed by a [B,N,H,D] buffer so that
     the caller's transpose back to [B,N,H*D] is free.  O_lo (bf16 only; empty for
     fp32) is O's bf16 rounding residual, saved for an accurate backward.
-    tile_mask is uint8 [B*H, ceil(N/32), ceil(N/64)] (32-query x 64-key sub-tile
-    activity).
+    Nmax (peak-tie counts) is formed only with_nmax, else returned empty: the
+    backward does not need it.  tile_mask is uint8 [B*H, ceil(N/32), ceil(N/64)]
+    (32-query x 64-key sub-tile activity).
     """
     B, H, N, D = q.shape
     code = _code(q, "flash")
@@ -210,30 +211,32 @@ def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma:
     o_lo = _new_o(q, o_bnhd) if bf else q.new_empty(0)
     M = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     Z = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
-    Nm = torch.empty((B, H, N), device=q.device, dtype=torch.int32)
+    Nm = torch.empty((B, H, N) if with_nmax else (0,), device=q.device, dtype=torch.int32)
     mask = torch.empty((B * H, (N + 31) // 32, (N + 63) // 64), device=q.device, dtype=torch.uint8)
     t32 = _tau32(tau)
     rc = _lib.lib().pnfx_flash_fwd(
         *_ptr4(q), *_ptr4(k), *_ptr4(v), *_ptr4(o), o_lo.data_ptr() if bf else None,
-        M.data_ptr(), Z.data_ptr(), Nm.data_ptr(), mask.data_ptr(), B, H, N, D,
+        M.data_ptr(), Z.data_ptr(), Nm.data_ptr() if with_nmax else None, mask.data_ptr(),
+        B, H, N, D,
         t32.data_ptr(), scale, gamma, int(has_gamma), int(causal), code, _stream(q))
     _lib.check(rc, "pnfx_flash_fwd")
     return o, o_lo, M, Z, Nm, mask
 
 
 @flash_fwd.register_fake
-def _(q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd):
+def _(q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd, with_nmax):
     B, H, N, D = q.shape
     o = _new_o(q, o_bnhd)
     o_lo = _new_o(q, o_bnhd) if q.dtype == torch.bfloat16 else q.new_empty(0)
     f = lambda dt: q.new_empty((B, H, N), dtype=dt)  # noqa: E731
+    nm = q.new_empty((B, H, N) if with_nmax else (0,), dtype=torch.int32)
     mask = q.new_empty((B * H, (N + 31) // 32, (N + 63) // 64), dtype=torch.uint8)
-    return o, o_lo, f(torch.float32), f(torch.float32), f(torch.int32), mask
+    return o, o_lo, f(torch.float32), f(torch.float32), nm, mask
 
 
 @torch.library.custom_op("pnfx::flash_bwd", mutates_args=(), device_types="cuda")
 def flash_bwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, o: Tensor, o_lo: Tensor, do: Tensor,
-              M: Tensor, Z: Tensor, Nmax: Tensor, mask: Tensor, scale: float, gamma: float,
+              M: Tensor, Z: Tensor, mask: Tensor, scale: float, gamma: float,
               has_gamma: bool, causal: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Deterministic flash backward; returns (dq, dk, dv, dtau) with dtau a 1-element fp32 tensor."""
     B, H, N, D = q.shape
@@ -255,7 +258,7 @@ def flash_bwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, o: Tensor, o_lo: Ten
     t32 = _tau32(tau)
     rc = L.pnfx_flash_bwd(
         *_ptr4(q), *_ptr4(k), *_ptr4(v), *_ptr4(o), o_lo.data_ptr() if use_lo else None,
-        *_ptr4(do), M.data_ptr(), Z.data_ptr(), Nmax.data_ptr(), mask.data_ptr(),
+        *_ptr4(do), M.data_ptr(), Z.data_ptr(), mask.data_ptr(),
         *_ptr4(dq), *_ptr4(dk), *_ptr4(dv), dtau.data_ptr(), ws.data_ptr(), ws_bytes, B, H, N, D,
         t32.data_ptr(), scale, gamma, int(has_gamma), int(causal), code, _stream(q))
     _lib.check(rc, "pnfx_flash_bwd")
@@ -263,7 +266,7 @@ def flash_bwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, o: Tensor, o_lo: Ten
 
 
 @flash_bwd.register_fake
-def _(q, k, v, tau, o, o_lo, do, M, Z, Nmax, mask, scale, gamma, has_gamma, causal):
+def _(q, k, v, tau, o, o_lo, do, M, Z, mask, scale, gamma, has_gamma, causal):
     return (torch.empty_like(q, memory_format=torch.contiguous_format),
             torch.empty_like(k, memory_format=torch.contiguous_format),
             torch.empty_like(v, memory_format=torch.contiguous_format),
@@ -271,16 +274,16 @@ def _(q, k, v, tau, o, o_lo, do, M, Z, Nmax, mask, scale, gamma, has_gamma, caus
 
 
 def _flash_setup(ctx, inputs, output):
-    q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd = inputs
+    q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd, with_nmax = inputs
     o, o_lo, M, Z, Nm, mask = output
-    ctx.save_for_backward(q, k, v, tau, o, o_lo, M, Z, Nm, mask)
+    ctx.save_for_backward(q, k, v, tau, o, o_lo, M, Z, mask)
     ctx.args = (scale, gamma, has_gamma, causal)
 
 
 def _flash_backward(ctx, do, do_lo, dM, dZ, dN, dmask):
-    q, k, v, tau, o, o_lo, M, Z, Nm, mask = ctx.saved_tensors
-    dq, dk, dv, dt = flash_bwd(q, k, v, tau, o, o_lo, do, M, Z, Nm, mask, *ctx.args)
-    return dq, dk, dv, dt.to(tau.dtype).view_as(tau), None, None, None, None, None
+    q, k, v, tau, o, o_lo, M, Z, mask = ctx.saved_tensors
+    dq, dk, dv, dt = flash_bwd(q, k, v, tau, o, o_lo, do, M, Z, mask, *ctx.args)
+    return dq, dk, dv, dt.to(tau.dtype).view_as(tau), None, None, None, None, None, None
 
 
 torch.library.register_autograd("pnfx::flash_fwd", _flash_backward, setup_context=_flash_setup)

@@ -112,6 +112,32 @@ def test_flash_stats_and_planted_ties(dev, dtype, scale):
             assert_bf16_close(to_np64(got), want, name)
         else:
             assert_close(to_np64(got), want, F32_TOL, F32_TOL, name)
+    tol = BF16_ATOL if dtype == torch.bfloat16 else F32_TOL
+    assert_sum_close(float(dtau), rdt, dabs, tol, "dtau")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_flash_rows_with_every_key_tied(dev, dtype):
+    """q = 0 and tau < 0 make every causal key of a row tie at the peak u = -tau (Nmax = i + 1)."""
+    B, H, N, D = 1, 2, 300, 64
+    q = seeded((B, H, N, D), 34, dtype, dev)
+    q[:, :, 100:] = 0
+    k = seeded((B, H, N, D), 35, dtype, dev)
+    v = seeded((B, H, N, D), 36, dtype, dev)
+    dO = seeded((B, H, N, D), 37, dtype, dev)
+    tau = -0.2
+    o, M, Z, Nm, mask = flash_pn_fir_tau_attention_with_stats(q, k, v, torch.tensor(tau, device=dev))
+    Of, Mo, Zo, No, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, tau, dO, 1 / 8, 0.5, True)
+    assert np.array_equal(No[0, 0, 100:], np.arange(101, N + 1))
+    assert np.array_equal(Nm.cpu().numpy(), No)
+    o, dq, dk, dv, dtau = _run(q, k, v, tau, dO, 1 / 8, 0.5, True)
+    for name, got, want in (("O", o, Of), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        if dtype == torch.bfloat16:
+            assert_bf16_close(to_np64(got), want, name)
+        else:
+            assert_close(to_np64(got), want, F32_TOL, F32_TOL, name)
+    tol = BF16_ATOL if dtype == torch.bfloat16 else F32_TOL
+    assert_sum_close(float(dtau), rdt, dabs, tol, "dtau")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

@@ -123,7 +123,7 @@ def test_c_abi_library_exports_every_declared_symbol():
     lib = _lib.lib()
     for s in syms:
         assert hasattr(lib, s), s
-    assert lib.pnfx_abi_version() == 1
+    assert lib.pnfx_abi_version() == _lib.ABI_VERSION
 
 
 def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
@@ -145,6 +145,6 @@ def test_hip_ops_refuse_cpu_tensors():
 
     q = torch.randn(1, 1, 8, 16)
     with pytest.raises(Exception):
-        torch.ops.pnfx.flash_fwd(q, q, q, torch.tensor(0.0), 0.25, 0.5, True, True, False)
+        torch.ops.pnfx.flash_fwd(q, q, q, torch.tensor(0.0), 0.25, 0.5, True, True, False, False)
     with pytest.raises(RuntimeError):
         P.flash_pn_fir_tau_attention(q, q, q, torch.tensor(0.0))
