@@ -40,51 +40,57 @@ __device__ __forceinline__ int perm_row(int blk, int r) {
 
 __device__ __forceinline__ bf16x8 ld16(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
-// LDS tiles are unpadded and XOR-swizzled on the 16-byte chunk index of each row.  The
-// swizzles are linear over GF(2) in the row bits and were chosen (exhaustive model of the
-// access patterns, 32- and 64-bank LDS) so that the MFMA fragment reads are conflict free
-// and the staging stores at most 2-way:
-//  * row-major tiles [rows][DK] are read as 16 permuted rows x 4 chunk groups;
+// LDS tiles are unpadded and XOR-swizzled on the 16-byte chunk index of each row, with
+// swizzles linear over GF(2) in the row bits.  They were chosen by measuring the LDS
+// bank-conflict counter for every access pattern of the kernels (a b128 read is conflict
+// free when each 16-lane group reads 16 consecutive tile rows at chunks g ^ swz(row)):
+//  * row-major tiles [rows][DK] store logical row R at slot slot_of(R), which places the
+//    16 rows of an MFMA fragment (rows perm_row(blk, 0..15)) in consecutive slots
+//    16 blk .. 16 blk + 15;
 //  * transposed tiles [D][64] are read as 16 consecutive rows x 4 chunk groups and written
 //    one 4-byte key pair at a time.
 // Linearity lets a fragment's swizzle split into a per-lane part and a compile-time part.
 __device__ __forceinline__ constexpr int parity6(int x) { return __builtin_popcount(x & 63) & 1; }
-__device__ __forceinline__ constexpr int swz_rows(int row) {
-  return parity6(row & 41) | (parity6(row & 52) << 1) | (parity6(row & 42) << 2);
-}
 __device__ __forceinline__ constexpr int swz_cols(int d) {
   return parity6(d & 18) | (parity6(d & 39) << 1) | (parity6(d & 12) << 2);
 }
+// Row-major tiles: 64-column rows use swz_cols; 128-column rows (16 chunks) a 4-bit swizzle.
 template <int DK>
-__device__ __forceinline__ constexpr int chunk_mask() {
-  return (DK / 8 < 8 ? DK / 8 : 8) - 1;
+__device__ __forceinline__ constexpr int swz_rt(int slot) {
+  return DK == 128 ? (parity6(slot & 46) | (parity6(slot & 10) << 1) | (parity6(slot & 28) << 2) |
+                      (parity6(slot & 13) << 3))
+                   : swz_cols(slot) & (DK / 8 - 1);
+}
+// Slot of logical row R: rows perm_row(blk, r) -> 16 blk + r.
+__device__ __forceinline__ constexpr int slot_of(int R) {
+  return 16 * (2 * (R >> 5) + ((R >> 2) & 1)) + 4 * ((R >> 3) & 3) + (R & 3);
 }
 
-// Element offset of 16-byte chunk `chunk` of row `row` in a row-major tile of DK columns.
+// Element offset of 16-byte chunk `chunk` of logical row `row` in a row-major tile of DK
+// columns.
 template <int DK>
 __device__ __forceinline__ int rt_off(int row, int chunk) {
-  return row * DK + ((chunk ^ (swz_rows(row) & chunk_mask<DK>())) << 3);
+  const int slot = slot_of(row);
+  return slot * DK + ((chunk ^ swz_rt<DK>(slot)) << 3);
 }
 // Element offset of keys 8*kc .. 8*kc+7 of row d in a transposed [D][64] tile.
 __device__ __forceinline__ int tt_off(int d, int kc) { return d * 64 + ((kc ^ swz_cols(d)) << 3); }
 
-// Fragment addressing with the lane part hoisted.  A row-major fragment reads row
-// perm_row(blk, r16) = rowc(blk) + rowl(r16) (disjoint bits) at chunk g + 4*ks:
-//   offset = rowc*DK + rowl*DK + (((g ^ swz(rowl)) ^ (4*ks ^ swz(rowc))) << 3).
+// Fragment addressing with the lane part hoisted.  A row-major fragment reads logical row
+// perm_row(blk, r16), i.e. slot 16 blk + r16 (disjoint bits), at chunk g + 4*ks:
+//   offset = 16 blk DK + r16 DK + (((g ^ swz(r16)) ^ (4 ks ^ swz(16 blk))) << 3).
 struct FragLane {
-  int rbase;  // rowl * DK   (row-major) or r16 * 64 (transposed)
+  int rbase;  // r16 * DK (row-major) or r16 * 64 (transposed)
   int x;      // g ^ swizzle(lane row part)
 };
 template <int DK>
 __device__ __forceinline__ FragLane rt_lane(int r16, int g) {
-  const int rowl = 8 * (r16 >> 2) + (r16 & 3);
-  return FragLane{rowl * DK, g ^ (swz_rows(rowl) & chunk_mask<DK>())};
+  return FragLane{r16 * DK, g ^ swz_rt<DK>(r16)};
 }
 template <int DK>
 __device__ __forceinline__ int rt_frag(const FragLane& fl, int blk, int ks) {
-  const int rowc = 32 * (blk >> 1) + 4 * (blk & 1);
-  const int cc = (4 * ks) ^ (swz_rows(rowc) & chunk_mask<DK>());
-  return rowc * DK + fl.rbase + ((fl.x ^ cc) << 3);
+  const int cc = (4 * ks) ^ swz_rt<DK>(16 * blk);
+  return 16 * blk * DK + fl.rbase + ((fl.x ^ cc) << 3);
 }
 __device__ __forceinline__ FragLane tt_lane(int r16, int g) {
   return FragLane{r16 * 64, g ^ swz_cols(r16)};
@@ -733,9 +739,9 @@ __device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], c
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int lr = perm_row(2 * hf + qq, 4 * g + i);
-      const f32x4 c0 = RCc[2 * lr];
+      const f32x4 c0 = RCc[2 * lr + (lr >> 3)];
       const float rM = c0[0], rr = c0[1], rcoef = c0[2], rD = c0[3];
-      const float rG = RCc[2 * lr + 1][0];
+      const float rG = RCc[2 * lr + (lr >> 3) + 1][0];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         float u = PS ? relu_mfma(s[qq][kb][i]) : fmaxf(__builtin_fmaf(s[qq][kb][i], scale, ntau), 0.f);
@@ -768,7 +774,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(16))) bf16 dOs[NBUF][BMQ * DK];
   __shared__ __attribute__((aligned(16))) bf16 Qt[NBUF][D * BMQ];
   __shared__ __attribute__((aligned(16))) bf16 dOt[NBUF][D * BMQ];
-  __shared__ __attribute__((aligned(16))) f32x4 RC[NBUF][BMQ * 2];
+  // Row constants, two f32x4 per query row and 16 bytes of padding after every 8 rows: the
+  // reads broadcast one row per 16-lane group, and the padding keeps the four groups'
+  // rows in different banks.
+  __shared__ __attribute__((aligned(16))) f32x4 RC[NBUF][BMQ * 2 + BMQ / 8];
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
@@ -831,7 +840,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     qtl.store_cols(Qt[bb], tid);
     otl.template store_rows<DK>(dOs[bb], tid);
     otl.store_cols(dOt[bb], tid);
-    if (tid < 2 * BMQ) RC[bb][tid] = rcr;
+    if (tid < 2 * BMQ) RC[bb][tid + (tid >> 4)] = rcr;
   };
 #pragma unroll
   for (int bb = 0; bb < NBUF; ++bb) {
