@@ -44,11 +44,11 @@ __device__ __forceinline__ bf16x8 ld16(const bf16* p) { return *reinterpret_cast
 // swizzles linear over GF(2) in the row bits.  They were chosen by measuring the LDS
 // bank-conflict counter for every access pattern of the kernels (a b128 read is conflict
 // free when each 16-lane group reads 16 consecutive tile rows at chunks g ^ swz(row)):
-//  * row-major tiles [rows][DK] store logical row R at slot slot_of(R), which places the
-//    16 rows of an MFMA fragment (rows perm_row(blk, 0..15)) in consecutive slots
+//  * tiles are row-major [rows][DK] and store logical row R at slot slot_of(R), which places
+//    the 16 rows of an MFMA fragment (rows perm_row(blk, 0..15)) in consecutive slots
 //    16 blk .. 16 blk + 15;
-//  * transposed tiles [D][64] are read as 16 consecutive rows x 4 chunk groups and written
-//    one 4-byte key pair at a time.
+//  * the transposed operands (V^T, K^T, Q^T, dO^T) are read from the same row-major tiles
+//    with ds_read_tr16_b64, which transposes 16-bit elements across each 16-lane group.
 // Linearity lets a fragment's swizzle split into a per-lane part and a compile-time part.
 __device__ __forceinline__ constexpr int parity6(int x) { return __builtin_popcount(x & 63) & 1; }
 __device__ __forceinline__ constexpr int swz_cols(int d) {
@@ -73,15 +73,12 @@ __device__ __forceinline__ int rt_off(int row, int chunk) {
   const int slot = slot_of(row);
   return slot * DK + ((chunk ^ swz_rt<DK>(slot)) << 3);
 }
-// Element offset of keys 8*kc .. 8*kc+7 of row d in a transposed [D][64] tile.
-__device__ __forceinline__ int tt_off(int d, int kc) { return d * 64 + ((kc ^ swz_cols(d)) << 3); }
-
 // Fragment addressing with the lane part hoisted.  A row-major fragment reads logical row
 // perm_row(blk, r16), i.e. slot 16 blk + r16 (disjoint bits), at chunk g + 4*ks:
 //   offset = 16 blk DK + r16 DK + (((g ^ swz(r16)) ^ (4 ks ^ swz(16 blk))) << 3).
 struct FragLane {
-  int rbase;  // r16 * DK (row-major) or r16 * 64 (transposed)
-  int x;      // g ^ swizzle(lane row part)
+  int rbase;  // lane part of the element offset
+  int x;      // lane part of the chunk index (XOR-combined with the constant part)
 };
 template <int DK>
 __device__ __forceinline__ FragLane rt_lane(int r16, int g) {
@@ -92,26 +89,45 @@ __device__ __forceinline__ int rt_frag(const FragLane& fl, int blk, int ks) {
   const int cc = (4 * ks) ^ swz_rt<DK>(16 * blk);
   return 16 * blk * DK + fl.rbase + ((fl.x ^ cc) << 3);
 }
-__device__ __forceinline__ FragLane tt_lane(int r16, int g) {
-  return FragLane{r16 * 64, g ^ swz_cols(r16)};
+
+// Transposed fragment X^T[16 db + r16][rows 32 hf + 8 g + t], t = 0..7 (the A operand of the
+// second GEMM: V^T, K^T, Q^T or dO^T) from a row-major tile, as two ds_read_tr16_b64.  In
+// each 16-lane group, lane 4 e + q addresses row 32 hf + 8 g + 4 u + e at columns
+// 16 db + 4 q .. + 3 (u = 0, 1 for the two reads), and lane r16 = 4 q' + r' receives
+// column 16 db + r16 of the four rows addressed by lanes 4 e + q'.  Row 32 hf + 8 g + 4 u + e
+// sits in slot 16 (2 hf + u) + 4 g + e.
+template <int DK>
+__device__ __forceinline__ FragLane tr_lane(int lane) {
+  const int g = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+  const int sl = 4 * g + e;
+  return FragLane{sl * DK + 4 * (q & 1), (q >> 1) ^ swz_rt<DK>(sl)};
 }
-__device__ __forceinline__ int tt_frag(const FragLane& fl, int db, int hf) {
-  const int cc = (4 * hf) ^ swz_cols(16 * db);
-  return 16 * db * 64 + fl.rbase + ((fl.x ^ cc) << 3);
+__device__ __forceinline__ bf16x4 ld_tr(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p));
+}
+template <int DK>
+__device__ __forceinline__ bf16x8 tr_frag(const bf16* tile, const FragLane& fl, int hf, int db) {
+  bf16x4 h[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int sc = 16 * (2 * hf + u);
+    const int cc = (2 * db) ^ swz_rt<DK>(sc);
+    h[u] = ld_tr(tile + sc * DK + fl.rbase + ((fl.x ^ cc) << 3));
+  }
+  return __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 // Register-staged copy of rows [row0, row0 + ROWS) of an [N, D] bf16 slice (row stride sn).
 // Chunk c of a thread covers rows 2*(c / CPR) and 2*(c / CPR) + 1 at columns
 // 8*(c % CPR) .. +7 (CPR = D/8 chunks per row), so a wave's load instruction reads whole
 // contiguous rows.  load() issues the global reads into registers (rows >= N read as zero);
-// store_rows() writes them to a row-major tile and store_cols() to a transposed [D][ROWS]
-// tile -- one global read serves both LDS layouts.
+// store_rows() writes them to a row-major tile.
 template <int ROWS, int D>
 struct PairTile {
   static constexpr int CPR = D / 8;
   static constexpr int NCH = (ROWS / 2) * CPR;
   static constexpr int PER = (NCH + 255) / 256;
-  static_assert(ROWS == 64, "transposed tiles are 64 keys/rows wide");
+  static_assert(ROWS == 64, "tiles are 64 rows (the slot_of permutation)");
   u32x4 a[PER], b[PER];
 
   __device__ __forceinline__ void load(const bf16* src, int64_t sn, int row0, int N, int tid) {
@@ -136,21 +152,6 @@ struct PairTile {
         const int r = 2 * (c / CPR), ch = c % CPR;
         *reinterpret_cast<u32x4*>(dst + rt_off<DK>(r, ch)) = a[i];
         *reinterpret_cast<u32x4*>(dst + rt_off<DK>(r + 1, ch)) = b[i];
-      }
-    }
-  }
-  __device__ __forceinline__ void store_cols(bf16* dst, int tid) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = tid + 256 * i;
-      if (NCH % 256 == 0 || c < NCH) {
-        const int r = 2 * (c / CPR), col = 8 * (c % CPR);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t lo = (e & 1) ? (a[i][e >> 1] >> 16) : (a[i][e >> 1] & 0xffffu);
-          const uint32_t hi = (e & 1) ? (b[i][e >> 1] & 0xffff0000u) : (b[i][e >> 1] << 16);
-          *reinterpret_cast<uint32_t*>(dst + tt_off(col + e, r >> 3) + (r & 7)) = lo | hi;
-        }
       }
     }
   }
@@ -241,7 +242,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][BN * DK];
-  __shared__ __attribute__((aligned(16))) bf16 Vt[2][D * BN];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[2][BN * DK];
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
   const bool has_rows = qrow0 < N;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
-  const FragLane flr = rt_lane<DK>(r16, g), flt = tt_lane(r16, g);
+  const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
 
   bf16x8 qf[2][KS];
 #pragma unroll
@@ -304,7 +305,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
   kt.load(K, p.ksn, 0, N, tid);
   vt.load(V, p.vsn, 0, N, tid);
   kt.template store_rows<DK>(Ks[0], tid);
-  vt.store_cols(Vt[0], tid);
+  vt.template store_rows<DK>(Vs[0], tid);
 
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = t * BN;
@@ -318,7 +319,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
     bool active = false;
     if (has_rows && !(CAUSAL && n0 > qrow0 + 31)) {
       const bf16* Kc = Ks[cur];
-      const bf16* Vc = Vt[cur];
+      const bf16* Vc = Vs[cur];
       const bool masked = (CAUSAL && n0 + BN - 1 > qrow0) || n0 + BN > N;
       // Two 32-key halves: each half's scores are exactly one k-step of the P.V MFMA.
 #pragma unroll
@@ -364,7 +365,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
         }
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16x8 vf = ld16(Vc + tt_frag(flt, db, hf));
+          const bf16x8 vf = tr_frag<DK>(Vc, flt, hf, db);
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(vf, pf[qb], acc[db][qb]);
         }
@@ -376,7 +377,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
     if (mrow && lane == 0) mrow[t] = active ? 1 : 0;
     if (pre) {
       kt.template store_rows<DK>(Ks[cur ^ 1], tid);
-      vt.store_cols(Vt[cur ^ 1], tid);
+      vt.template store_rows<DK>(Vs[cur ^ 1], tid);
     }
   }
   if (mrow && lane == 0)
@@ -526,10 +527,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
-  constexpr int NBUF = D <= 64 ? 2 : 1;
+  constexpr int NBUF = 2;
   __shared__ __attribute__((aligned(16))) bf16 Ks[NBUF][BN * DK];
   __shared__ __attribute__((aligned(16))) bf16 Vs[NBUF][BN * DK];
-  __shared__ __attribute__((aligned(16))) bf16 Kt[NBUF][D * BN];
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
@@ -547,7 +547,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   const bool has_rows = qrow0 < N;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
-  const FragLane flr = rt_lane<DK>(r16, g), flt = tt_lane(r16, g);
+  const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
   int* const wflag = p.flags + ((int64_t)bh * nqb + qblk) * 4;
   if (MODE == DQ_FIX && (wflag[0] | wflag[1] | wflag[2] | wflag[3]) == 0) return;  // whole block
 
@@ -605,7 +605,6 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   kt.load(K, p.ksn, 0, N, tid);
   vt.load(V, p.vsn, 0, N, tid);
   kt.template store_rows<DK>(Ks[0], tid);
-  kt.store_cols(Kt[0], tid);
   vt.template store_rows<DK>(Vs[0], tid);
 
   for (int t = 0; t < ntiles; ++t) {
@@ -621,7 +620,6 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
     if (work) {
       const bf16* Kc = Ks[cur];
       const bf16* Vc = Vs[cur];
-      const bf16* Ktc = Kt[cur];
       const bool masked = (CAUSAL && n0 + BN - 1 > qrow0) || n0 + BN > N;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -662,7 +660,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
                          dw[1][qb][1], dw[1][qb][2], dw[1][qb][3]);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16x8 ktf = ld16(Ktc + tt_frag(flt, db, hf));
+          const bf16x8 ktf = tr_frag<DK>(Kc, flt, hf, db);
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(ktf, pf[qb], acc[db][qb]);
         }
@@ -674,7 +672,6 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       if (NBUF == 1) __syncthreads();
       const int nxt = NBUF == 2 ? cur ^ 1 : 0;
       kt.template store_rows<DK>(Ks[nxt], tid);
-      kt.store_cols(Kt[nxt], tid);
       vt.template store_rows<DK>(Vs[nxt], tid);
     }
   }
@@ -769,11 +766,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
-  constexpr int NBUF = D <= 64 ? 2 : 1;
+  constexpr int NBUF = 2;
   __shared__ __attribute__((aligned(16))) bf16 Qs[NBUF][BMQ * DK];
   __shared__ __attribute__((aligned(16))) bf16 dOs[NBUF][BMQ * DK];
-  __shared__ __attribute__((aligned(16))) bf16 Qt[NBUF][D * BMQ];
-  __shared__ __attribute__((aligned(16))) bf16 dOt[NBUF][D * BMQ];
   // Row constants, two f32x4 per query row and 16 bytes of padding after every 8 rows: the
   // reads broadcast one row per 16-lane group, and the padding keeps the four groups'
   // rows in different banks.
@@ -795,7 +790,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const bool has_keys = kw0 < N;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
-  const FragLane flr = rt_lane<DK>(r16, g), flt = tt_lane(r16, g);
+  const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
 
   bf16x8 kf[KB][KS], vf[KB][KS];
 #pragma unroll
@@ -837,9 +832,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   };
   auto store_tile = [&](int bb) {
     qtl.template store_rows<DK>(Qs[bb], tid);
-    qtl.store_cols(Qt[bb], tid);
     otl.template store_rows<DK>(dOs[bb], tid);
-    otl.store_cols(dOt[bb], tid);
     if (tid < 2 * BMQ) RC[bb][tid + (tid >> 4)] = rcr;
   };
 #pragma unroll
@@ -868,8 +861,6 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     if (work) {
       const bf16* Qc = Qs[cur];
       const bf16* dOc = dOs[cur];
-      const bf16* Qtc = Qt[cur];
-      const bf16* dOtc = dOt[cur];
       const bool masked = (CAUSAL && m0 < kw0 + KPW - 1) || m0 + BMQ > N || kw0 + KPW > N;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -910,9 +901,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         }
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const int toff = tt_frag(flt, db, hf);
-          const bf16x8 ot = ld16(dOtc + toff);
-          const bf16x8 qt_ = ld16(Qtc + toff);
+          const bf16x8 ot = tr_frag<DK>(dOc, flt, hf, db);
+          const bf16x8 qt_ = tr_frag<DK>(Qc, flt, hf, db);
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
             adv[db][kb] = mfma16x16x32(ot, wf[kb], adv[db][kb]);
