@@ -595,6 +595,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   const int ntiles = (kv_end + BN - 1) / BN;
   const uint8_t* mrow =
       (p.mask && has_rows) ? p.mask + ((int64_t)bh * p.nq32 + (qrow0 >> 5)) * p.nk64 : nullptr;
+  // The activity byte of the next tile is fetched one iteration ahead and kept as a raw
+  // byte until it is tested, so that its wait does not also wait for the tile prefetch.
+  int act_next = mrow ? mrow[0] : 1;
 
   PairTile<BN, D> kt, vt;
 #pragma unroll
@@ -616,7 +619,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       kt.load(K, p.ksn, n0 + BN, N, tid);
       vt.load(V, p.vsn, n0 + BN, N, tid);
     }
-    const bool work = has_rows && !(CAUSAL && n0 > qrow0 + 31) && !(mrow && mrow[t] == 0);
+    const int act = act_next;
+    if (mrow && pre) act_next = mrow[t + 1];
+    const bool work = has_rows && !(CAUSAL && n0 > qrow0 + 31) && act != 0;
     if (work) {
       const bf16* Kc = Ks[cur];
       const bf16* Vc = Vs[cur];
@@ -845,19 +850,25 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     store_tile(0);
   }
 
+  // Activity of a 64-row query tile for this wave's keys: either of its two 32-row halves.
+  // Fetched one iteration ahead and kept as raw bytes until tested, so that its wait does
+  // not also wait for the tile prefetch.
+  int act_next[2] = {1, 0};
+  auto fetch_active = [&](int m) {
+    const int r32 = m >> 5;
+    act_next[0] = mcol[(int64_t)r32 * p.nk64];
+    act_next[1] = r32 + 1 < p.nq32 ? mcol[(int64_t)(r32 + 1) * p.nk64] : 0;
+  };
+  if (mcol && qt0 < nqt) fetch_active(qt0 * BMQ);
   for (int qt = qt0; qt < nqt; ++qt) {
     const int m0 = qt * BMQ;
     const int cur = NBUF == 2 ? ((qt - qt0) & 1) : 0;
     __syncthreads();
     const bool pre = qt + 1 < nqt;
     if (pre) load_tile(m0 + BMQ);
-    bool work = has_keys && !(CAUSAL && m0 + BMQ - 1 < kw0);
-    if (work && mcol) {
-      const int r32 = m0 >> 5;
-      const bool a0 = mcol[(int64_t)r32 * p.nk64] != 0;
-      const bool a1 = (r32 + 1 < p.nq32) && mcol[(int64_t)(r32 + 1) * p.nk64] != 0;
-      work = a0 || a1;
-    }
+    const int act0 = act_next[0], act1 = act_next[1];
+    if (mcol && pre) fetch_active(m0 + BMQ);
+    const bool work = has_keys && !(CAUSAL && m0 + BMQ - 1 < kw0) && (act0 | act1) != 0;
     if (work) {
       const bf16* Qc = Qs[cur];
       const bf16* dOc = dOs[cur];
