@@ -374,11 +374,12 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
       }
       active = __any(active);
     }
-    if (mrow && lane == 0) mrow[t] = active ? 1 : 0;
     if (pre) {
       kt.template store_rows<DK>(Ks[cur ^ 1], tid);
       vt.template store_rows<DK>(Vs[cur ^ 1], tid);
     }
+    // After the LDS stores: their wait for the tile prefetch then does not include this store.
+    if (mrow && lane == 0) mrow[t] = active ? 1 : 0;
   }
   if (mrow && lane == 0)
     for (int t = ntiles; t < p.nk64; ++t) mrow[t] = 0;
