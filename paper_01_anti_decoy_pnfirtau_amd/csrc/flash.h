@@ -28,7 +28,7 @@ struct BwdParams {
   const float* M;
   const float* Z;
   const uint8_t* mask;
-  float* rc;         // row constants [B*H*N][8]: M, r = g/Z, c = 10 g/Z * scale, Dv, G
+  float* rc;         // row constants [B*H*N][8], layout private to each dtype's kernels
   double* partials;  // tau partials, one per wave of the dq kernel (bf16: [B*H][N/128][4])
   int* flags;        // per dq wave: some row has two or more peak ties
   float* dtau;

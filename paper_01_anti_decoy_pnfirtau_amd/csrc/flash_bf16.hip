@@ -430,10 +430,14 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
 
 // ------------------------------------------------------------------------------ backward
 // Row constants: D_i = <dO_i, O_i> / g_i (the flash identity of src/triton_pnfirtau.py:575-577),
-// r = g/Z, c = 10 g/Z * scale, and G = D gamma/(M+gamma)^2 * scale, the gradient of the
+// c = 10 g/Z * scale, and G = D gamma/(M+gamma)^2 * scale, the gradient of the
 // gate through the peak for the whole row (zero on silent rows and without a gate).  The
 // Nmax keys tied at the peak share it, G/Nmax each (src/triton_pnfirtau.py:580-586); the
 // dQ kernel counts the ties and stores G/Nmax in place of G for the dK/dV kernel.
+// For the dK/dV kernel the weights are rescaled: with rho = (g/Z)^(1/10) and a = rho u,
+// w = u^10 g/Z = a^10 and c u^9 (dW - D) = a^9 (kappa dW - kappa D), kappa = 10 scale rho,
+// which saves two multiplies per score (and a <= 1, so no power overflows).
+// Layout per row: {M, rho, kappa, -kappa D}, {G, c, D, 0}.
 template <int D, bool HAS_GAMMA>
 __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   constexpr int LPR = D / 8;  // lanes per row
@@ -473,8 +477,10 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
       const float dgate = p.gamma / ((M + p.gamma) * (M + p.gamma));
       G = Dv * dgate * p.scale;
     }
-    f32x4 c0 = {M, g / Z, 10.f * g / Z * p.scale, Dv};
-    f32x4 c1 = {G, 0.f, 0.f, 0.f};
+    const float rho = powf(g / Z, 0.1f);  // 0 on silent rows
+    const float kappa = 10.f * p.scale * rho;
+    f32x4 c0 = {M, rho, kappa, -kappa * Dv};
+    f32x4 c1 = {G, 10.f * g / Z * p.scale, Dv, 0.f};
     reinterpret_cast<f32x4*>(p.rc)[2 * row] = c0;
     reinterpret_cast<f32x4*>(p.rc)[2 * row + 1] = c1;
   }
@@ -571,8 +577,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       c1 = reinterpret_cast<const f32x4*>(p.rc)[2 * ((int64_t)bh * N + row) + 1];
     }
     rM[qb] = c0[0];
-    rc[qb] = c0[2];
-    rD[qb] = c0[3];
+    rc[qb] = c1[1];
+    rD[qb] = c1[2];
     rG[qb] = c1[0];
   }
 
@@ -743,7 +749,7 @@ __device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], c
     for (int i = 0; i < 4; ++i) {
       const int lr = perm_row(2 * hf + qq, 4 * g + i);
       const f32x4 c0 = RCc[2 * lr + (lr >> 3)];
-      const float rM = c0[0], rr = c0[1], rcoef = c0[2], rD = c0[3];
+      const float rM = c0[0], rho = c0[1], kappa = c0[2], nkD = c0[3];
       const float rG = RCc[2 * lr + (lr >> 3) + 1][0];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
@@ -753,13 +759,13 @@ __device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], c
           const int key = kw0 + 16 * kb + r16;
           if ((causal && key > qrow) || key >= N || qrow >= N) u = 0.f;
         }
-        const float u2 = u * u;
-        const float u4 = u2 * u2;
-        const float u8 = u4 * u4;
-        const float u9 = u8 * u;
-        s[qq][kb][i] = u8 * u2 * rr;  // w = P g / Z
+        const float a = u * rho;
+        const float a2 = a * a;
+        const float a4 = a2 * a2;
+        const float a9 = a4 * a4 * a;
+        s[qq][kb][i] = a9 * a;  // w = P g / Z
         const float tie = (u == rM) ? rG : 0.f;
-        dw[qq][kb][i] = __builtin_fmaf(rcoef * u9, dw[qq][kb][i] - rD, tie);
+        dw[qq][kb][i] = __builtin_fmaf(a9, __builtin_fmaf(kappa, dw[qq][kb][i], nkD), tie);
       }
     }
   }

@@ -152,11 +152,15 @@ def _(dw, raw, tau, M, Z, Nmax, scale, p, gamma, has_gamma, causal):
 def _rows_setup(ctx, inputs, output):
     raw, tau, scale, p, gamma, has_gamma, causal = inputs
     _, M, Z, Nm = output
+    ctx.mark_non_differentiable(M, Z, Nm)
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(raw, tau, M, Z, Nm)
     ctx.args = (scale, p, gamma, has_gamma, causal)
 
 
 def _rows_backward(ctx, dw, dM, dZ, dN):
+    if dw is None:  # W did not reach the loss
+        return (None,) * 7
     raw, tau, M, Z, Nm = ctx.saved_tensors
     d, dt = pn_rows_bwd(dw, raw, tau, M, Z, Nm, *ctx.args)
     # fp64 sum of the row partials, as src/triton_pnfirtau.py:784
@@ -276,11 +280,16 @@ def _(q, k, v, tau, o, o_lo, do, M, Z, mask, scale, gamma, has_gamma, causal):
 def _flash_setup(ctx, inputs, output):
     q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd, with_nmax = inputs
     o, o_lo, M, Z, Nm, mask = output
+    # Only O carries a gradient: no zero-filled gradients are materialised for the rest.
+    ctx.mark_non_differentiable(o_lo, M, Z, Nm, mask)
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(q, k, v, tau, o, o_lo, M, Z, mask)
     ctx.args = (scale, gamma, has_gamma, causal)
 
 
 def _flash_backward(ctx, do, do_lo, dM, dZ, dN, dmask):
+    if do is None:  # O did not reach the loss
+        return (None,) * 10
     q, k, v, tau, o, o_lo, M, Z, mask = ctx.saved_tensors
     dq, dk, dv, dt = flash_bwd(q, k, v, tau, o, o_lo, do, M, Z, mask, *ctx.args)
     return dq, dk, dv, dt.to(tau.dtype).view_as(tau), None, None, None, None, None, None
