@@ -520,15 +520,12 @@ __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2],
 // tiles software-pipelined through LDS (double-buffered when it fits).
 //
 // Peak ties.  A key tied at the row's peak gets the extra gradient G/Nmax.  The forward
-// does not count ties, so this kernel runs as two passes.  DQ_COUNT: the tie term uses the
-// whole-row G per tied key while the ties are counted (one compare serves both); afterwards
-// G/Nmax replaces G in the row constants (for the dK/dV kernel), the tau partial is
-// corrected to G per row, and each wave flags whether any of its rows had two or more ties.
-// DQ_FIX: only workgroups with a flagged wave run; they recompute dQ with G/Nmax (on
-// typical inputs every row has a single peak and nothing is flagged).
-enum { DQ_COUNT = 0, DQ_FIX = 1 };
-
-template <int D, bool CAUSAL, bool PS, int MODE>
+// does not count ties, so the first pass over the keys uses the whole-row G per tied key
+// while it counts the ties (one compare serves both).  Afterwards G/Nmax replaces G in the
+// row constants (for the dK/dV kernel) and the tau partial is corrected to G per row.  A row
+// with two or more ties got too much tie gradient in dQ: if the workgroup has any such row
+// (rare: duplicated keys), it runs the key loop a second time with G/Nmax.
+template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   constexpr int BM = 128, BN = 64;
   constexpr int DK = D < 32 ? 32 : D;
@@ -555,8 +552,6 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   const float ntau = -p.tau[0];
   const float scale = p.scale;
   const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
-  int* const wflag = p.flags + ((int64_t)bh * nqb + qblk) * 4;
-  if (MODE == DQ_FIX && (wflag[0] | wflag[1] | wflag[2] | wflag[3]) == 0) return;  // whole block
 
   bf16x8 qf[2][KS], dof[2][KS];
   float rM[2], rc[2], rD[2], rG[2];
@@ -583,7 +578,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   }
 
   const f32x4 s_init = PS ? f32x4{ntau, ntau, ntau, ntau} : f32x4{0.f, 0.f, 0.f, 0.f};
-  int cnt[2] = {0, 0};  // lane-local tie counts (DQ_COUNT)
+  int cnt[2] = {0, 0};  // lane-local tie counts (first pass)
   // Sum of every ds the wave forms, accumulated by the MFMA: a constant A fragment whose
   // row 0 is all ones turns the ds^T operand into its column sums (lanes g == 0, slot 0).
   f32x4 adt[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -604,7 +599,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       (p.mask && has_rows) ? p.mask + ((int64_t)bh * p.nq32 + (qrow0 >> 5)) * p.nk64 : nullptr;
   // The activity byte of the next tile is fetched one iteration ahead and kept as a raw
   // byte until it is tested, so that its wait does not also wait for the tile prefetch.
-  int act_next = mrow ? mrow[0] : 1;
+  int act_next;
 
   PairTile<BN, D> kt, vt;
 #pragma unroll
@@ -612,6 +607,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
     zero_pad_cols<BN, D, DK>(Ks[bb], tid);
     zero_pad_cols<BN, D, DK>(Vs[bb], tid);
   }
+  for (int pass = 0;; ++pass) {
+  act_next = mrow ? mrow[0] : 1;
   kt.load(K, p.ksn, 0, N, tid);
   vt.load(V, p.vsn, 0, N, tid);
   kt.template store_rows<DK>(Ks[0], tid);
@@ -658,13 +655,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
             dw[kk][qb] = c4;
           }
         }
-        constexpr bool COUNT = MODE == DQ_COUNT;
         if (masked)
-          ds_kq<true, PS, COUNT>(s, dw, cnt, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N,
-                                 CAUSAL, g, r16);
+          ds_kq<true, PS, true>(s, dw, cnt, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N,
+                                CAUSAL, g, r16);
         else
-          ds_kq<false, PS, COUNT>(s, dw, cnt, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N,
-                                  CAUSAL, g, r16);
+          ds_kq<false, PS, true>(s, dw, cnt, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N,
+                                 CAUSAL, g, r16);
         bf16x8 pf[2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -687,22 +683,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       vt.template store_rows<DK>(Vs[nxt], tid);
     }
   }
+  if (pass == 1) break;
 
-  bf16* dQ = static_cast<bf16*>(p.dq) + b * p.dqsb + h * p.dqsh;
-#pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int qrow = qrow0 + 16 * qb + r16;
-    if (qrow < N) {
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        bf16x4 o4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o4[i] = (bf16)acc[db][qb][i];
-        *reinterpret_cast<bf16x4*>(dQ + (int64_t)qrow * p.dqsn + 16 * db + 4 * g) = o4;
-      }
-    }
-  }
-  if (MODE == DQ_FIX) return;
   // Tie counts per row (the four lane groups of a row), G -> G/Nmax for the dK/dV kernel,
   // and the tau partial: the MFMA sum holds Nmax G per row for ties whose gradient is G.
   double dsum = g == 0 ? (double)adt[0][0] + (double)adt[1][0] : 0.0;
@@ -718,12 +700,32 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       if (c > 1) dsum -= (double)rG[qb] * (double)(c - 1);
     }
     multi = multi || (c > 1 && rG[qb] != 0.f);
+    rG[qb] = c > 0 ? rG[qb] / (float)c : 0.f;  // for a second pass
   }
   dsum = wave_sum_d(dsum);
-  multi = __any(multi);
-  if (lane == 0) {
-    p.partials[((int64_t)bh * nqb + qblk) * 4 + w] = dsum;
-    wflag[w] = multi ? 1 : 0;
+  if (lane == 0) p.partials[((int64_t)bh * nqb + qblk) * 4 + w] = dsum;
+  // Second pass only if some row of the workgroup has several ties (also a barrier: the
+  // last tile's LDS buffer is free before the first tile is staged again).
+  if (!__syncthreads_or(multi ? 1 : 0)) break;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) acc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  bf16* dQ = static_cast<bf16*>(p.dq) + b * p.dqsb + h * p.dqsh;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int qrow = qrow0 + 16 * qb + r16;
+    if (qrow < N) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        bf16x4 o4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o4[i] = (bf16)acc[db][qb][i];
+        *reinterpret_cast<bf16x4*>(dQ + (int64_t)qrow * p.dqsn + 16 * db + 4 * g) = o4;
+      }
+    }
   }
 }
 
@@ -1007,17 +1009,11 @@ int launch_fwd_d(const FwdParams& fp, bool causal, hipStream_t st) {
   return launch_status("pnfx_flash_fwd");
 }
 
-// The counting pass, then the fix-up pass (workgroups without a flagged wave exit at once).
 template <int D, bool PS>
 void launch_dq(const BwdParams& bp, bool causal, dim3 grid, hipStream_t st) {
   const dim3 block(256);
-  if (causal) {
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true, PS, DQ_COUNT>), grid, block, 0, st, bp);
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true, PS, DQ_FIX>), grid, block, 0, st, bp);
-  } else {
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false, PS, DQ_COUNT>), grid, block, 0, st, bp);
-    hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false, PS, DQ_FIX>), grid, block, 0, st, bp);
-  }
+  if (causal) hipLaunchKernelGGL((flash_bwd_dq_kernel<D, true, PS>), grid, block, 0, st, bp);
+  else hipLaunchKernelGGL((flash_bwd_dq_kernel<D, false, PS>), grid, block, 0, st, bp);
 }
 
 template <int D>

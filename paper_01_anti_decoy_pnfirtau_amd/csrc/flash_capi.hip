@@ -100,11 +100,10 @@ extern "C" int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int
   char* ws = static_cast<char*>(workspace);
   float* rcbuf = reinterpret_cast<float*>(ws);
   double* parts = reinterpret_cast<double*>(ws + wl.rc_bytes);
-  int* flags = reinterpret_cast<int*>(ws + wl.rc_bytes + wl.parts_bytes);
   BwdParams bp{q, k, v, o, o_lo, dout, dq, dk, dv,
                qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn, dosb, dosh, dosn,
                dqsb, dqsh, dqsn, dksb, dksh, dksn, dvsb, dvsh, dvsn,
-               M, Z, tile_mask, rcbuf, parts, flags, dtau,
+               M, Z, tile_mask, rcbuf, parts, dtau,
                (int)B, (int)H, (int)N, (int)((N + 31) / 32), (int)((N + 63) / 64),
                bwd_nkvb(N, D), tau, scale, gamma};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
