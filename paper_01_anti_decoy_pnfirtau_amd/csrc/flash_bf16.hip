@@ -210,10 +210,39 @@ __device__ __forceinline__ void map_block(int nblk, int BH, bool heavy_last_inde
 // the causal diagonal or N when MASK; returns the lane's per-query-row maximum in tm.
 // PS: the score scale is a power of two folded into the register-resident operand and -tau
 // into the MFMA accumulator, so s already holds q.k*scale - tau.
-template <bool MASK, bool PS>
-__device__ __forceinline__ void rectify_kq(f32x4 (&s)[2][2], float (&tm)[2], float scale, float ntau,
-                                           int n0, int hf, int qrow0, int N, bool causal, int g,
-                                           int r16) {
+// Scores in the key-major layout S^T (register i of lane group g holds key
+// perm_row(blk, 4g+i), lane r16 holds query 16qb+r16).  Without the scale fold, the scores
+// are first mapped to s*scale - tau (PS: the MFMA already produced that).
+template <bool PS>
+__device__ __forceinline__ void affine_kq(f32x4 (&s)[2][2], float scale, float ntau) {
+  if (PS) return;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[kk][qb][i] = __builtin_fmaf(s[kk][qb][i], scale, ntau);
+}
+
+// Causal and sequence-end mask, in place: entries outside it become -1, which the rectifier
+// maps to 0.  Only tiles that straddle the diagonal or the sequence end run it, so the
+// common tile's score code has no mask operations and no second copy.
+__device__ __forceinline__ void mask_kq(f32x4 (&s)[2][2], int n0, int hf, int qrow0, int N,
+                                        bool causal, int g, int r16) {
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = n0 + perm_row(2 * hf + kk, 4 * g + i);
+        const int qrow = qrow0 + 16 * qb + r16;
+        if ((causal && key > qrow) || key >= N) s[kk][qb][i] = -1.f;
+      }
+}
+
+// Rectify in place and take each query's lane-local maximum.
+__device__ __forceinline__ void rectify_kq(f32x4 (&s)[2][2], float (&tm)[2]) {
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     float mx = 0.f;
@@ -221,12 +250,7 @@ __device__ __forceinline__ void rectify_kq(f32x4 (&s)[2][2], float (&tm)[2], flo
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float u = PS ? relu_mfma(s[kk][qb][i]) : fmaxf(__builtin_fmaf(s[kk][qb][i], scale, ntau), 0.f);
-        if (MASK) {
-          const int key = n0 + perm_row(2 * hf + kk, 4 * g + i);
-          const int qrow = qrow0 + 16 * qb + r16;
-          if ((causal && key > qrow) || key >= N) u = 0.f;
-        }
+        const float u = relu_mfma(s[kk][qb][i]);
         s[kk][qb][i] = u;
         mx = fmaxf(mx, u);
       }
@@ -340,10 +364,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
           }
         }
         float tm[2];
-        if (masked)
-          rectify_kq<true, PS>(s, tm, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
-        else
-          rectify_kq<false, PS>(s, tm, scale, ntau, n0, hf, qrow0, N, CAUSAL, g, r16);
+        affine_kq<PS>(s, scale, ntau);
+        if (masked) mask_kq(s, n0, hf, qrow0, N, CAUSAL, g, r16);
+        rectify_kq(s, tm);
         if (!__any(fmaxf(tm[0], tm[1]) > 0.f)) continue;  // silent half: skip P and P.V
         active = true;
         bf16x8 pf[2];
@@ -489,24 +512,17 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
 // dS for the 16 scores a lane holds in one 32-key half tile of the dQ kernel (S^T layout,
 // one query row per lane), written over dw: (c u^9)(dW - D) + [u == M] G.  COUNT also
 // counts the peak ties per query block.
-template <bool MASK, bool PS, bool COUNT>
+template <bool COUNT>
 __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2], int (&cnt)[2],
                                       const float (&rM)[2], const float (&rc)[2],
-                                      const float (&rD)[2], const float (&rG)[2], float scale,
-                                      float ntau, int n0, int hf, int qrow0, int N, bool causal,
-                                      int g, int r16) {
+                                      const float (&rD)[2], const float (&rG)[2]) {
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float u = PS ? relu_mfma(s[kk][qb][i]) : fmaxf(__builtin_fmaf(s[kk][qb][i], scale, ntau), 0.f);
-        if (MASK) {
-          const int key = n0 + perm_row(2 * hf + kk, 4 * g + i);
-          const int qrow = qrow0 + 16 * qb + r16;
-          if ((causal && key > qrow) || key >= N) u = 0.f;
-        }
+        const float u = relu_mfma(s[kk][qb][i]);
         const float u2 = u * u;
         const float u4 = u2 * u2;
         const float u9 = u4 * u4 * u;
@@ -655,12 +671,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
             dw[kk][qb] = c4;
           }
         }
-        if (masked)
-          ds_kq<true, PS, true>(s, dw, cnt, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N,
-                                CAUSAL, g, r16);
-        else
-          ds_kq<false, PS, true>(s, dw, cnt, rM, rc, rD, rG, scale, ntau, n0, hf, qrow0, N,
-                                 CAUSAL, g, r16);
+        affine_kq<PS>(s, scale, ntau);
+        if (masked) mask_kq(s, n0, hf, qrow0, N, CAUSAL, g, r16);
+        ds_kq<true>(s, dw, cnt, rM, rc, rD, rG);
         bf16x8 pf[2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -741,10 +754,39 @@ struct DkdvCfg {
 
 // In the S layout (key per lane, four query rows per 16-row block), for one 32-row half
 // (query blocks 2*hf, 2*hf+1): w = u^10 g/Z written over s and ds written over dw.
-template <bool MASK, int KB, bool PS>
-__device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const f32x4* RCc,
-                                        float scale, float ntau, int m0, int hf, int kw0, int N,
+// Query-major layout S (register i of lane group g holds query perm_row(blk, 4g+i) of the
+// tile, lane r16 holds key 16kb+r16 of the wave's keys): the affine map and the mask, as
+// affine_kq and mask_kq above.
+template <int KB, bool PS>
+__device__ __forceinline__ void affine_qk(f32x4 (&s)[2][KB], float scale, float ntau) {
+  if (PS) return;
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[qq][kb][i] = __builtin_fmaf(s[qq][kb][i], scale, ntau);
+}
+
+template <int KB>
+__device__ __forceinline__ void mask_qk(f32x4 (&s)[2][KB], int m0, int hf, int kw0, int N,
                                         bool causal, int g, int r16) {
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int qrow = m0 + perm_row(2 * hf + qq, 4 * g + i);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int key = kw0 + 16 * kb + r16;
+        if ((causal && key > qrow) || key >= N || qrow >= N) s[qq][kb][i] = -1.f;
+      }
+    }
+}
+
+template <int KB>
+__device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const f32x4* RCc,
+                                        int hf, int g) {
 #pragma unroll
   for (int qq = 0; qq < 2; ++qq) {
 #pragma unroll
@@ -755,12 +797,7 @@ __device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], c
       const float rG = RCc[2 * lr + (lr >> 3) + 1][0];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        float u = PS ? relu_mfma(s[qq][kb][i]) : fmaxf(__builtin_fmaf(s[qq][kb][i], scale, ntau), 0.f);
-        if (MASK) {
-          const int qrow = m0 + lr;
-          const int key = kw0 + 16 * kb + r16;
-          if ((causal && key > qrow) || key >= N || qrow >= N) u = 0.f;
-        }
+        const float u = relu_mfma(s[qq][kb][i]);
         const float a = u * rho;
         const float a2 = a * a;
         const float a4 = a2 * a2;
@@ -907,10 +944,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
             dw[qq][kb] = c4;
           }
         }
-        if (masked)
-          w_ds_qk<true, KB, PS>(s, dw, RC[cur], scale, ntau, m0, hf, kw0, N, CAUSAL, g, r16);
-        else
-          w_ds_qk<false, KB, PS>(s, dw, RC[cur], scale, ntau, m0, hf, kw0, N, CAUSAL, g, r16);
+        affine_qk<KB, PS>(s, scale, ntau);
+        if (masked) mask_qk<KB>(s, m0, hf, kw0, N, CAUSAL, g, r16);
+        w_ds_qk<KB>(s, dw, RC[cur], hf, g);
         bf16x8 wf[KB], sf[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
