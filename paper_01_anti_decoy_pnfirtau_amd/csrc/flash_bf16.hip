@@ -452,15 +452,23 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
 }
 
 // ------------------------------------------------------------------------------ backward
-// Row constants: D_i = <dO_i, O_i> / g_i (the flash identity of src/triton_pnfirtau.py:575-577),
-// c = 10 g/Z * scale, and G = D gamma/(M+gamma)^2 * scale, the gradient of the
-// gate through the peak for the whole row (zero on silent rows and without a gate).  The
-// Nmax keys tied at the peak share it, G/Nmax each (src/triton_pnfirtau.py:580-586); the
-// dQ kernel counts the ties and stores G/Nmax in place of G for the dK/dV kernel.
-// For the dK/dV kernel the weights are rescaled: with rho = (g/Z)^(1/10) and a = rho u,
-// w = u^10 g/Z = a^10 and c u^9 (dW - D) = a^9 (kappa dW - kappa D), kappa = 10 scale rho,
-// which saves two multiplies per score (and a <= 1, so no power overflows).
-// Layout per row: {M, rho, kappa, -kappa D}, {G, c, D, 0}.
+// Row constants.  With D_i = <dO_i, O_i>/g_i (the flash identity of
+// src/triton_pnfirtau.py:575-577) and x_i = g_i/Z_i, the score gradient (:580-586) is
+//   dS_ij = 10 scale x_i [u_ij^9 (dW_ij - D_i) + [u_ij == M_i] G''_i/Nmax_i],
+//   G''_i = D_i gate'(M_i) / (10 x_i),
+// which is how the dQ kernel forms it: the dW MFMA accumulator starts at -D_i, the bracket
+// costs one FMA per score after the power chain, and the row factor 10 scale x_i is applied
+// to dQ and to the tau partials once, at the end.  The dK/dV kernel needs the row factor
+// inside its sums over rows; there, with rho_i = x_i^(1/10), a = rho u and
+// kappa_i = 10 scale rho_i, the dV weight is w = u^10 x = a^10 and
+//   dS_ij = a^9 (kappa_i dW_ij - kappa_i D_i) + [u_ij == M_i] G_i/Nmax_i,
+//   G_i = D_i gate'(M_i) scale.
+// The bf16 row constants are eight planes of N floats per (b, h): M, -D, G'', x, rho, kappa,
+// -kappa D, and G/Nmax (written by the dQ kernel, which counts the ties).
+__device__ __forceinline__ float* rc_plane(const BwdParams& p, int64_t bh, int k) {
+  return p.rc + (bh * 8 + k) * (int64_t)p.N;
+}
+
 template <int D, bool HAS_GAMMA>
 __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   constexpr int LPR = D / 8;  // lanes per row
@@ -470,17 +478,15 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   const int part = tid % LPR;
   const int64_t total = (int64_t)p.B * p.H * p.N;
   float dot = 0.f;
-  int64_t bh = 0, i = 0;
   if (row < total) {
-    bh = row / p.N;
-    i = row % p.N;
+    const int64_t bh = row / p.N, i = row % p.N;
     const int64_t b = bh / p.H, h = bh % p.H;
     const int64_t ooff = b * p.osb + h * p.osh + i * p.osn + 8 * part;
     const u32x4 ov = *reinterpret_cast<const u32x4*>(static_cast<const bf16*>(p.o) + ooff);
     u32x4 lv = {0u, 0u, 0u, 0u};
     if (p.o_lo) lv = *reinterpret_cast<const u32x4*>(static_cast<const bf16*>(p.o_lo) + ooff);
-    const u32x4 dv =
-        *reinterpret_cast<const u32x4*>(static_cast<const bf16*>(p.dout) + b * p.dosb + h * p.dosh + i * p.dosn + 8 * part);
+    const u32x4 dv = *reinterpret_cast<const u32x4*>(static_cast<const bf16*>(p.dout) + b * p.dosb +
+                                                     h * p.dosh + i * p.dosn + 8 * part);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float o0 = __uint_as_float(ov[e] << 16) + __uint_as_float(lv[e] << 16);
@@ -494,28 +500,29 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   if (row < total && part == 0) {
     const float M = p.M[row], Z = p.Z[row];
     const float g = M > 0.f ? (HAS_GAMMA ? M / (M + p.gamma) : 1.f) : 0.f;
+    const float x = g / Z;  // 0 on silent rows
     const float Dv = g > 0.f ? dot / g : 0.f;
-    float G = 0.f;
-    if (HAS_GAMMA && M > 0.f) {
-      const float dgate = p.gamma / ((M + p.gamma) * (M + p.gamma));
-      G = Dv * dgate * p.scale;
-    }
-    const float rho = powf(g / Z, 0.1f);  // 0 on silent rows
+    float dgate = 0.f;
+    if (HAS_GAMMA && M > 0.f) dgate = p.gamma / ((M + p.gamma) * (M + p.gamma));
+    const float rho = powf(x, 0.1f);
     const float kappa = 10.f * p.scale * rho;
-    f32x4 c0 = {M, rho, kappa, -kappa * Dv};
-    f32x4 c1 = {G, 10.f * g / Z * p.scale, Dv, 0.f};
-    reinterpret_cast<f32x4*>(p.rc)[2 * row] = c0;
-    reinterpret_cast<f32x4*>(p.rc)[2 * row + 1] = c1;
+    const int64_t bh = row / p.N, i = row % p.N;
+    rc_plane(p, bh, 0)[i] = M;
+    rc_plane(p, bh, 1)[i] = -Dv;
+    rc_plane(p, bh, 2)[i] = x > 0.f ? Dv * dgate / (10.f * x) : 0.f;
+    rc_plane(p, bh, 3)[i] = x;
+    rc_plane(p, bh, 4)[i] = rho;
+    rc_plane(p, bh, 5)[i] = kappa;
+    rc_plane(p, bh, 6)[i] = -kappa * Dv;
   }
 }
 
-// dS for the 16 scores a lane holds in one 32-key half tile of the dQ kernel (S^T layout,
-// one query row per lane), written over dw: (c u^9)(dW - D) + [u == M] G.  COUNT also
-// counts the peak ties per query block.
+// dS/(10 scale x) for the 16 scores a lane holds in one 32-key half tile of the dQ kernel
+// (S^T layout, one query row per lane), written over dw = dW - D: u^9 dw + [u == M] G''.
+// COUNT also counts the peak ties per query block.
 template <bool COUNT>
 __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2], int (&cnt)[2],
-                                      const float (&rM)[2], const float (&rc)[2],
-                                      const float (&rD)[2], const float (&rG)[2]) {
+                                      const float (&rM)[2], const float (&rG)[2]) {
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -526,8 +533,8 @@ __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2],
         const float u2 = u * u;
         const float u4 = u2 * u2;
         const float u9 = u4 * u4 * u;
-        const bool tie = u == rM[qb];  // rG = 0 on silent rows
-        dw[kk][qb][i] = __builtin_fmaf(rc[qb] * u9, dw[kk][qb][i] - rD[qb], tie ? rG[qb] : 0.f);
+        const bool tie = u == rM[qb];  // G'' = 0 on silent rows
+        dw[kk][qb][i] = __builtin_fmaf(u9, dw[kk][qb][i], tie ? rG[qb] : 0.f);
         if (COUNT) cnt[qb] += tie ? 1 : 0;
       }
 }
@@ -567,10 +574,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   const bool has_rows = qrow0 < N;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
+  const float ds_mult = 10.f * scale;  // the score loops form dS/(10 scale x)
   const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
 
   bf16x8 qf[2][KS], dof[2][KS];
-  float rM[2], rc[2], rD[2], rG[2];
+  float rM[2], rG[2], rX[2];
+  f32x4 dw_init[2];  // -D: the dW accumulator starts there
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const int row = qrow0 + 16 * qb + r16;
@@ -582,15 +591,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       dof[qb][ks] = ok ? ld16(dO + (int64_t)row * p.dosn + col) : zero_bf16x8();
       if (PS) qf[qb][ks] = scale_frag(qf[qb][ks], scale);
     }
-    f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
-    if (row < N) {
-      c0 = reinterpret_cast<const f32x4*>(p.rc)[2 * ((int64_t)bh * N + row)];
-      c1 = reinterpret_cast<const f32x4*>(p.rc)[2 * ((int64_t)bh * N + row) + 1];
-    }
-    rM[qb] = c0[0];
-    rc[qb] = c1[1];
-    rD[qb] = c1[2];
-    rG[qb] = c1[0];
+    const bool ok = row < N;
+    rM[qb] = ok ? rc_plane(p, bh, 0)[row] : 0.f;
+    const float nxd = ok ? rc_plane(p, bh, 1)[row] : 0.f;
+    rG[qb] = ok ? rc_plane(p, bh, 2)[row] : 0.f;
+    rX[qb] = ok ? rc_plane(p, bh, 3)[row] : 0.f;
+    dw_init[qb] = f32x4{nxd, nxd, nxd, nxd};
   }
 
   const f32x4 s_init = PS ? f32x4{ntau, ntau, ntau, ntau} : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -661,7 +667,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
           }
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
-            f32x4 a4 = s_init, c4 = {0.f, 0.f, 0.f, 0.f};
+            f32x4 a4 = s_init, c4 = dw_init[qb];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
               a4 = mfma16x16x32(kf[ks], qf[qb][ks], a4);
@@ -673,7 +679,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
         }
         affine_kq<PS>(s, scale, ntau);
         if (masked) mask_kq(s, n0, hf, qrow0, N, CAUSAL, g, r16);
-        ds_kq<true>(s, dw, cnt, rM, rc, rD, rG);
+        ds_kq<true>(s, dw, cnt, rM, rG);
         bf16x8 pf[2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -698,9 +704,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   }
   if (pass == 1) break;
 
-  // Tie counts per row (the four lane groups of a row), G -> G/Nmax for the dK/dV kernel,
-  // and the tau partial: the MFMA sum holds Nmax G per row for ties whose gradient is G.
-  double dsum = g == 0 ? (double)adt[0][0] + (double)adt[1][0] : 0.0;
+  // Tie counts per row (the four lane groups of a row), G/Nmax for the dK/dV kernel, and
+  // the tau partial: the MFMA sum holds Nmax G'' per row for ties whose gradient is G''.
+  double dsum = 0.0;
   bool multi = false;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
@@ -709,13 +715,15 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
     c += __shfl_xor(c, 32, 64);
     const int qrow = qrow0 + 16 * qb + r16;
     if (g == 0 && qrow < N) {
-      p.rc[8 * ((int64_t)bh * N + qrow) + 4] = c > 0 ? rG[qb] / (float)c : 0.f;
-      if (c > 1) dsum -= (double)rG[qb] * (double)(c - 1);
+      rc_plane(p, bh, 7)[qrow] = c > 0 ? rG[qb] * (ds_mult * rX[qb]) / (float)c : 0.f;
+      double rs = (double)adt[qb][0];
+      if (c > 1) rs -= (double)rG[qb] * (double)(c - 1);
+      dsum += rs * (double)rX[qb];
     }
     multi = multi || (c > 1 && rG[qb] != 0.f);
     rG[qb] = c > 0 ? rG[qb] / (float)c : 0.f;  // for a second pass
   }
-  dsum = wave_sum_d(dsum);
+  dsum = wave_sum_d(dsum) * (double)ds_mult;
   if (lane == 0) p.partials[((int64_t)bh * nqb + qblk) * 4 + w] = dsum;
   // Second pass only if some row of the workgroup has several ties (also a barrier: the
   // last tile's LDS buffer is free before the first tile is staged again).
@@ -730,12 +738,13 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const int qrow = qrow0 + 16 * qb + r16;
+    const float rowf = ds_mult * rX[qb];
     if (qrow < N) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         bf16x4 o4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o4[i] = (bf16)acc[db][qb][i];
+        for (int i = 0; i < 4; ++i) o4[i] = (bf16)(acc[db][qb][i] * rowf);
         *reinterpret_cast<bf16x4*>(dQ + (int64_t)qrow * p.dqsn + 16 * db + 4 * g) = o4;
       }
     }
@@ -784,29 +793,31 @@ __device__ __forceinline__ void mask_qk(f32x4 (&s)[2][KB], int m0, int hf, int k
     }
 }
 
+// The dV weight w = a^10 over s and dS = a^9 (kappa dW - kappa D) + [u == M] G/Nmax over dw,
+// a = rho u.  rc holds the planes (M, rho, kappa, -kappa D, G/Nmax) of the tile's rows, each
+// `pitch` floats; rows r4 + 4 qq + (0..3) are the four query rows a lane's registers cover in
+// the 16-row block qq.
 template <int KB>
-__device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const f32x4* RCc,
-                                        int hf, int g) {
+__device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const float* rc,
+                                        int pitch, int r4) {
 #pragma unroll
   for (int qq = 0; qq < 2; ++qq) {
+    f32x4 c[5];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int lr = perm_row(2 * hf + qq, 4 * g + i);
-      const f32x4 c0 = RCc[2 * lr + (lr >> 3)];
-      const float rM = c0[0], rho = c0[1], kappa = c0[2], nkD = c0[3];
-      const float rG = RCc[2 * lr + (lr >> 3) + 1][0];
+    for (int k = 0; k < 5; ++k) c[k] = *reinterpret_cast<const f32x4*>(rc + k * pitch + r4 + 4 * qq);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const float u = relu_mfma(s[qq][kb][i]);
-        const float a = u * rho;
+        const float a = u * c[1][i];
         const float a2 = a * a;
         const float a4 = a2 * a2;
         const float a9 = a4 * a4 * a;
-        s[qq][kb][i] = a9 * a;  // w = P g / Z
-        const float tie = (u == rM) ? rG : 0.f;
-        dw[qq][kb][i] = __builtin_fmaf(a9, __builtin_fmaf(kappa, dw[qq][kb][i], nkD), tie);
+        s[qq][kb][i] = a9 * a;
+        const float tie = (u == c[0][i]) ? c[4][i] : 0.f;  // G = 0 on silent rows
+        dw[qq][kb][i] = __builtin_fmaf(a9, __builtin_fmaf(c[2][i], dw[qq][kb][i], c[3][i]), tie);
       }
-    }
   }
 }
 
@@ -820,10 +831,11 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   constexpr int NBUF = 2;
   __shared__ __attribute__((aligned(16))) bf16 Qs[NBUF][BMQ * DK];
   __shared__ __attribute__((aligned(16))) bf16 dOs[NBUF][BMQ * DK];
-  // Row constants, two f32x4 per query row and 16 bytes of padding after every 8 rows: the
-  // reads broadcast one row per 16-lane group, and the padding keeps the four groups'
-  // rows in different banks.
-  __shared__ __attribute__((aligned(16))) f32x4 RC[NBUF][BMQ * 2 + BMQ / 8];
+  // Row constants as five planes (M, rho, kappa, -kappa D, G/Nmax) of the tile's rows: a lane
+  // reads the four consecutive rows its registers cover as one f32x4 per plane (broadcast
+  // within a 16-lane group; the four groups' rows are 8 apart, in different banks).
+  constexpr int NPL = 5;
+  __shared__ __attribute__((aligned(16))) float RCp[NBUF][NPL][BMQ];
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
@@ -835,7 +847,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const bf16* K = static_cast<const bf16*>(p.k) + b * p.ksb + h * p.ksh;
   const bf16* V = static_cast<const bf16*>(p.v) + b * p.vsb + h * p.vsh;
   const bf16* dO = static_cast<const bf16*>(p.dout) + b * p.dosb + h * p.dosh;
-  const f32x4* RCg = reinterpret_cast<const f32x4*>(p.rc) + 2 * (int64_t)bh * N;
+  // Staging of the row constants: thread t covers plane (t / 64) and, for t < 64, also
+  // plane 4 (planes 0, 4, 5, 6, 7 of the workspace: M, rho, kappa, -kappa D, G/Nmax).
+  const float* RCg0 = rc_plane(p, bh, tid < BMQ ? 0 : 3 + tid / BMQ);
+  const float* RCg1 = rc_plane(p, bh, 7);
   const int kv0 = kvb * BNK;
   const int kw0 = kv0 + KPW * w;
   const bool has_keys = kw0 < N;
@@ -872,19 +887,19 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const uint8_t* mcol = (p.mask && has_keys) ? p.mask + (int64_t)bh * p.nq32 * p.nk64 + ktile : nullptr;
 
   PairTile<BMQ, D> qtl, otl;
-  f32x4 rcr = {0.f, 0.f, 0.f, 0.f};
+  float rcr0 = 0.f, rcr1 = 0.f;
   auto load_tile = [&](int m) {
     qtl.load(Q, p.qsn, m, N, tid);
     otl.load(dO, p.dosn, m, N, tid);
-    if (tid < 2 * BMQ) {
-      const int row = m + (tid >> 1);
-      rcr = row < N ? RCg[2 * row + (tid & 1)] : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    const int row = m + (tid & (BMQ - 1));
+    rcr0 = row < N ? RCg0[row] : 0.f;
+    if (tid < BMQ) rcr1 = row < N ? RCg1[row] : 0.f;
   };
   auto store_tile = [&](int bb) {
     qtl.template store_rows<DK>(Qs[bb], tid);
     otl.template store_rows<DK>(dOs[bb], tid);
-    if (tid < 2 * BMQ) RC[bb][tid + (tid >> 4)] = rcr;
+    RCp[bb][tid / BMQ][tid & (BMQ - 1)] = rcr0;
+    if (tid < BMQ) RCp[bb][4][tid] = rcr1;
   };
 #pragma unroll
   for (int bb = 0; bb < NBUF; ++bb) {
@@ -946,7 +961,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         }
         affine_qk<KB, PS>(s, scale, ntau);
         if (masked) mask_qk<KB>(s, m0, hf, kw0, N, CAUSAL, g, r16);
-        w_ds_qk<KB>(s, dw, RC[cur], hf, g);
+        // rows 32 hf + 8 g + 4 qq + (0..3) of the tile are perm_row(2 hf + qq, 4 g + i)
+        w_ds_qk<KB>(s, dw, &RCp[cur][0][0], BMQ, 32 * hf + 8 * g);
         bf16x8 wf[KB], sf[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
