@@ -304,6 +304,7 @@ def main():
     q5, k5, v5, dO5 = make_inputs(B5, H5, N5, D5, 1, dev, std=D5 ** -0.25)
     wall5, ev5 = time_steps(flash_step_fn(q5, k5, v5, dO5, 0.0), max(3, args.steps // 2), 2)
     flops5 = 7 * gemm_flops(B5, H5, N5, D5)
+    kern5 = kernel_times(q5, k5, v5, dO5, 0.0, max(3, args.steps // 4))
     del q5, k5, v5, dO5
 
     cpu = None if args.no_cpu_baseline else cpu_baseline()
@@ -337,7 +338,8 @@ def main():
                       "speedup": round(wall_ms / wall_s, 3)},
         "fir": fir,
         "wide_head": {"config": C5, "ms_per_step": round(wall5, 4),
-                      "tflops": round(flops5 / (wall5 * 1e-3) / 1e12, 2)},
+                      "tflops": round(flops5 / (wall5 * 1e-3) / 1e12, 2),
+                      "kernel_ms": {n: r["ms"] for n, r in kern5.items()}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -548,8 +548,11 @@ __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2],
 // row constants (for the dK/dV kernel) and the tau partial is corrected to G per row.  A row
 // with two or more ties got too much tie gradient in dQ: if the workgroup has any such row
 // (rare: duplicated keys), it runs the key loop a second time with G/Nmax.
+// At D = 128 the dQ accumulators and the Q/dO fragments need more than the 256 registers a
+// wave has at two workgroups per CU: one workgroup per CU gives each wave 512 (VGPRs plus
+// AGPRs) and no spills, which is far faster than spilling.
 template <int D, bool CAUSAL, bool PS>
-__global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdParams p) {
   constexpr int BM = 128, BN = 64;
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
