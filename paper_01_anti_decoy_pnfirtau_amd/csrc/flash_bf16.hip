@@ -157,6 +157,55 @@ struct PairTile {
   }
 };
 
+// Direct global -> LDS staging of a 64-row tile (rows row0 .. row0 + 63 of an [N, D] bf16
+// slice with row stride sn) into the swizzled row-major layout, with global_load_lds_dwordx4:
+// no register staging and no LDS store instructions.  Each such load writes 16 bytes per
+// lane to LDS at (wave-uniform base) + 16 * lane, so a wave fills 64 consecutive chunks; each
+// lane loads the global chunk that belongs at its position (the layout is a permutation of
+// the tile's chunks).  The per-lane row and column are fixed at construction.  Rows >= N
+// re-load row N - 1 and the padding chunks of D < DK re-load a real chunk of the row: both
+// only ever meet masked scores or zero MFMA operands, so any finite value serves.  The
+// caller waits for the loads (vmcnt) before the barrier that publishes the tile.
+// Direct global -> LDS copy of 16 bytes per lane (lane l lands at dst + 8 l).  (The builtin
+// sits in a plain function: called directly from a class template's member, it kept the
+// host pass from emitting some of the kernels' launch stubs.)
+__device__ __forceinline__ void lds_dma16(const bf16* src, bf16* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+__device__ __forceinline__ int row_of_slot(int s) {  // inverse of slot_of
+  return (s & 32) | ((s & 12) << 1) | ((s >> 2) & 4) | (s & 3);
+}
+template <int D, int DK>
+struct TileDma {
+  static constexpr int CPR = DK / 8;      // 16-byte chunks per tile row
+  static constexpr int NI = 64 * CPR / 256;  // loads per thread
+  int row[NI], col[NI];
+  __device__ __forceinline__ TileDma(int w, int lane) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int L = (4 * j + w) * 64 + lane;  // chunk index in the tile
+      const int slot = L / CPR, pos = L % CPR;
+      const int ch = pos ^ swz_rt<DK>(slot);
+      row[j] = row_of_slot(slot);
+      col[j] = 8 * (ch % (D / 8));
+    }
+  }
+  __device__ __forceinline__ void load(const bf16* src, int64_t sn, int row0, int N, bf16* tile,
+                                       int w) const {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int r = min(row0 + row[j], N - 1);
+      lds_dma16(src + (int64_t)r * sn + col[j], tile + (4 * j + w) * 512);
+    }
+  }
+};
+// Direct global -> LDS copy of 4 bytes per lane (lane l lands at dst + l).
+__device__ __forceinline__ void lds_dma4(const float* src, float* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
+}
+// Wait for this wave's outstanding global loads (including direct-to-LDS ones).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Zero the k-padding chunks [D/8, DK/8) of a row-major tile (the 32-wide MFMA when D < 32).
 template <int ROWS, int D, int DK>
 __device__ __forceinline__ void zero_pad_cols(bf16* dst, int tid) {
@@ -824,6 +873,13 @@ __device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], c
   }
 }
 
+// One LDS buffer of the dK/dV kernel: a query tile of Q and dO and its row-constant planes.
+struct QBuf {
+  bf16* q;
+  bf16* o;
+  float* rc;  // [planes][64 rows]
+};
+
 template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   constexpr int KPW = DkdvCfg<D>::KPW, KB = DkdvCfg<D>::KB, BNK = DkdvCfg<D>::BNK;
@@ -831,14 +887,20 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
-  constexpr int NBUF = 2;
-  __shared__ __attribute__((aligned(16))) bf16 Qs[NBUF][BMQ * DK];
-  __shared__ __attribute__((aligned(16))) bf16 dOs[NBUF][BMQ * DK];
-  // Row constants as five planes (M, rho, kappa, -kappa D, G/Nmax) of the tile's rows: a lane
-  // reads the four consecutive rows its registers cover as one f32x4 per plane (broadcast
-  // within a 16-lane group; the four groups' rows are 8 apart, in different banks).
+  // Two LDS buffers, as separate objects: the compiler then knows that the direct-to-LDS
+  // loads filling one buffer do not write the other, and does not make the reads of the
+  // current tile wait for the prefetch of the next one.  Row constants are five planes
+  // (M, rho, kappa, -kappa D, G/Nmax) of the tile's rows: a lane reads the four consecutive
+  // rows its registers cover as one f32x4 per plane (broadcast within a 16-lane group; the
+  // four groups' rows are 8 apart, in different banks).
   constexpr int NPL = 5;
-  __shared__ __attribute__((aligned(16))) float RCp[NBUF][NPL][BMQ];
+  __shared__ __attribute__((aligned(16))) bf16 Qs0[BMQ * DK];
+  __shared__ __attribute__((aligned(16))) bf16 dOs0[BMQ * DK];
+  __shared__ __attribute__((aligned(16))) float RC0[NPL * BMQ];
+  __shared__ __attribute__((aligned(16))) bf16 Qs1[BMQ * DK];
+  __shared__ __attribute__((aligned(16))) bf16 dOs1[BMQ * DK];
+  __shared__ __attribute__((aligned(16))) float RC1[NPL * BMQ];
+  const QBuf buf0{Qs0, dOs0, RC0}, buf1{Qs1, dOs1, RC1};
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
@@ -850,10 +912,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const bf16* K = static_cast<const bf16*>(p.k) + b * p.ksb + h * p.ksh;
   const bf16* V = static_cast<const bf16*>(p.v) + b * p.vsb + h * p.vsh;
   const bf16* dO = static_cast<const bf16*>(p.dout) + b * p.dosb + h * p.dosh;
-  // Staging of the row constants: thread t covers plane (t / 64) and, for t < 64, also
-  // plane 4 (planes 0, 4, 5, 6, 7 of the workspace: M, rho, kappa, -kappa D, G/Nmax).
-  const float* RCg0 = rc_plane(p, bh, tid < BMQ ? 0 : 3 + tid / BMQ);
-  const float* RCg1 = rc_plane(p, bh, 7);
+  // Staging of the row constants (planes 0, 4, 5, 6, 7 of the workspace: M, rho, kappa,
+  // -kappa D, G/Nmax): wave w copies plane w of the tile's rows, wave 0 also the last.
+  const float* RCgw = rc_plane(p, bh, w == 0 ? 0 : 3 + w);
+  const float* RCg4 = rc_plane(p, bh, 7);
   const int kv0 = kvb * BNK;
   const int kw0 = kv0 + KPW * w;
   const bool has_keys = kw0 < N;
@@ -889,30 +951,17 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const int ktile = kw0 >> 6;  // 64-key tile of this wave's keys (forward mask column)
   const uint8_t* mcol = (p.mask && has_keys) ? p.mask + (int64_t)bh * p.nq32 * p.nk64 + ktile : nullptr;
 
-  PairTile<BMQ, D> qtl, otl;
-  float rcr0 = 0.f, rcr1 = 0.f;
-  auto load_tile = [&](int m) {
-    qtl.load(Q, p.qsn, m, N, tid);
-    otl.load(dO, p.dosn, m, N, tid);
-    const int row = m + (tid & (BMQ - 1));
-    rcr0 = row < N ? RCg0[row] : 0.f;
-    if (tid < BMQ) rcr1 = row < N ? RCg1[row] : 0.f;
+  // Tiles go straight from global memory to LDS buffer bb; rows >= N repeat row N - 1 (their
+  // scores are masked), including their row constants.
+  const TileDma<D, DK> tdma(w, lane);
+  auto load_tile = [&](int m, const QBuf& bb) {
+    tdma.load(Q, p.qsn, m, N, bb.q, w);
+    tdma.load(dO, p.dosn, m, N, bb.o, w);
+    const int row = min(m + lane, N - 1);
+    lds_dma4(RCgw + row, bb.rc + w * BMQ);
+    if (w == 0) lds_dma4(RCg4 + row, bb.rc + (NPL - 1) * BMQ);
   };
-  auto store_tile = [&](int bb) {
-    qtl.template store_rows<DK>(Qs[bb], tid);
-    otl.template store_rows<DK>(dOs[bb], tid);
-    RCp[bb][tid / BMQ][tid & (BMQ - 1)] = rcr0;
-    if (tid < BMQ) RCp[bb][4][tid] = rcr1;
-  };
-#pragma unroll
-  for (int bb = 0; bb < NBUF; ++bb) {
-    zero_pad_cols<BMQ, D, DK>(Qs[bb], tid);
-    zero_pad_cols<BMQ, D, DK>(dOs[bb], tid);
-  }
-  if (qt0 < nqt) {
-    load_tile(qt0 * BMQ);
-    store_tile(0);
-  }
+  if (qt0 < nqt) load_tile(qt0 * BMQ, buf0);
 
   // Activity of a 64-row query tile for this wave's keys: either of its two 32-row halves.
   // Fetched one iteration ahead and kept as raw bytes until tested, so that its wait does
@@ -924,18 +973,19 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     act_next[1] = r32 + 1 < p.nq32 ? mcol[(int64_t)(r32 + 1) * p.nk64] : 0;
   };
   if (mcol && qt0 < nqt) fetch_active(qt0 * BMQ);
-  for (int qt = qt0; qt < nqt; ++qt) {
+  // One query tile: computed from buffer bc while the next tile streams into buffer bn.
+  auto step = [&](int qt, const QBuf& bc, const QBuf& bn) {
     const int m0 = qt * BMQ;
-    const int cur = NBUF == 2 ? ((qt - qt0) & 1) : 0;
+    wait_vmem();  // this wave's part of tile qt is in LDS
     __syncthreads();
     const bool pre = qt + 1 < nqt;
-    if (pre) load_tile(m0 + BMQ);
+    if (pre) load_tile(m0 + BMQ, bn);
     const int act0 = act_next[0], act1 = act_next[1];
     if (mcol && pre) fetch_active(m0 + BMQ);
     const bool work = has_keys && !(CAUSAL && m0 + BMQ - 1 < kw0) && (act0 | act1) != 0;
     if (work) {
-      const bf16* Qc = Qs[cur];
-      const bf16* dOc = dOs[cur];
+      const bf16* Qc = bc.q;
+      const bf16* dOc = bc.o;
       const bool masked = (CAUSAL && m0 < kw0 + KPW - 1) || m0 + BMQ > N || kw0 + KPW > N;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -965,7 +1015,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         affine_qk<KB, PS>(s, scale, ntau);
         if (masked) mask_qk<KB>(s, m0, hf, kw0, N, CAUSAL, g, r16);
         // rows 32 hf + 8 g + 4 qq + (0..3) of the tile are perm_row(2 hf + qq, 4 g + i)
-        w_ds_qk<KB>(s, dw, &RCp[cur][0][0], BMQ, 32 * hf + 8 * g);
+        w_ds_qk<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
         bf16x8 wf[KB], sf[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
@@ -986,10 +1036,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         }
       }
     }
-    if (pre) {
-      if (NBUF == 1) __syncthreads();
-      store_tile(NBUF == 2 ? cur ^ 1 : 0);
-    }
+  };
+  for (int qt = qt0; qt < nqt; qt += 2) {
+    step(qt, buf0, buf1);
+    if (qt + 1 < nqt) step(qt + 1, buf1, buf0);
   }
 
   bf16* dK = static_cast<bf16*>(p.dk) + b * p.dksb + h * p.dksh;
