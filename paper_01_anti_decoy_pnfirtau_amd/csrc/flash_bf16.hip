@@ -203,6 +203,19 @@ struct TileDma {
 __device__ __forceinline__ void lds_dma4(const float* src, float* dst) {
   __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
 }
+// One LDS buffer of the forward and dQ kernels: a key tile of K and V.
+struct KVBuf {
+  bf16* k;
+  bf16* v;
+};
+
+// One LDS buffer of the dK/dV kernel: a query tile of Q and dO and its row-constant planes.
+struct QBuf {
+  bf16* q;
+  bf16* o;
+  float* rc;  // [planes][64 rows]
+};
+
 // Wait for this wave's outstanding global loads (including direct-to-LDS ones).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -314,8 +327,13 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][BN * DK];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[2][BN * DK];
+  // Two K/V tile buffers as separate LDS objects (see the dK/dV kernel), filled straight
+  // from global memory.
+  __shared__ __attribute__((aligned(16))) bf16 Ks0[BN * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Vs0[BN * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Ks1[BN * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Vs1[BN * DK];
+  const KVBuf buf0{Ks0, Vs0}, buf1{Ks1, Vs1};
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
@@ -370,29 +388,23 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
   uint8_t* mrow =
       (p.mask && has_rows) ? p.mask + ((int64_t)bh * p.nq32 + (qrow0 >> 5)) * p.nk64 : nullptr;
 
-  // Software pipeline: tile t+1 is read from HBM/L2 into registers while tile t is
-  // computed from LDS, then committed to the other LDS buffer; one barrier per tile.
-  PairTile<BN, D> kt, vt;
-  zero_pad_cols<BN, D, DK>(Ks[0], tid);
-  zero_pad_cols<BN, D, DK>(Ks[1], tid);
-  kt.load(K, p.ksn, 0, N, tid);
-  vt.load(V, p.vsn, 0, N, tid);
-  kt.template store_rows<DK>(Ks[0], tid);
-  vt.template store_rows<DK>(Vs[0], tid);
-
-  for (int t = 0; t < ntiles; ++t) {
+  // Software pipeline: tile t+1 streams from HBM/L2 straight into one LDS buffer while tile
+  // t is computed from the other; one barrier per tile.
+  const TileDma<D, DK> tdma(w, lane);
+  auto load_tile = [&](int n, const KVBuf& bb) {
+    tdma.load(K, p.ksn, n, N, bb.k, w);
+    tdma.load(V, p.vsn, n, N, bb.v, w);
+  };
+  auto step = [&](int t, const KVBuf& bc, const KVBuf& bn) {
     const int n0 = t * BN;
-    const int cur = t & 1;
+    wait_vmem();  // this wave's part of tile t is in LDS
     __syncthreads();
     const bool pre = t + 1 < ntiles;
-    if (pre) {
-      kt.load(K, p.ksn, n0 + BN, N, tid);
-      vt.load(V, p.vsn, n0 + BN, N, tid);
-    }
+    if (pre) load_tile(n0 + BN, bn);
     bool active = false;
     if (has_rows && !(CAUSAL && n0 > qrow0 + 31)) {
-      const bf16* Kc = Ks[cur];
-      const bf16* Vc = Vs[cur];
+      const bf16* Kc = bc.k;
+      const bf16* Vc = bc.v;
       const bool masked = (CAUSAL && n0 + BN - 1 > qrow0) || n0 + BN > N;
       // Two 32-key halves: each half's scores are exactly one k-step of the P.V MFMA.
 #pragma unroll
@@ -446,12 +458,12 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
       }
       active = __any(active);
     }
-    if (pre) {
-      kt.template store_rows<DK>(Ks[cur ^ 1], tid);
-      vt.template store_rows<DK>(Vs[cur ^ 1], tid);
-    }
-    // After the LDS stores: their wait for the tile prefetch then does not include this store.
     if (mrow && lane == 0) mrow[t] = active ? 1 : 0;
+  };
+  load_tile(0, buf0);
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, buf0, buf1);
+    if (t + 1 < ntiles) step(t + 1, buf1, buf0);
   }
   if (mrow && lane == 0)
     for (int t = ntiles; t < p.nk64; ++t) mrow[t] = 0;
@@ -606,9 +618,13 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
-  constexpr int NBUF = 2;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[NBUF][BN * DK];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[NBUF][BN * DK];
+  // Two K/V tile buffers as separate LDS objects (see the dK/dV kernel), filled straight
+  // from global memory.
+  __shared__ __attribute__((aligned(16))) bf16 Ks0[BN * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Vs0[BN * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Ks1[BN * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Vs1[BN * DK];
+  const KVBuf buf0{Ks0, Vs0}, buf1{Ks1, Vs1};
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
@@ -675,34 +691,24 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
   // byte until it is tested, so that its wait does not also wait for the tile prefetch.
   int act_next;
 
-  PairTile<BN, D> kt, vt;
-#pragma unroll
-  for (int bb = 0; bb < NBUF; ++bb) {
-    zero_pad_cols<BN, D, DK>(Ks[bb], tid);
-    zero_pad_cols<BN, D, DK>(Vs[bb], tid);
-  }
-  for (int pass = 0;; ++pass) {
-  act_next = mrow ? mrow[0] : 1;
-  kt.load(K, p.ksn, 0, N, tid);
-  vt.load(V, p.vsn, 0, N, tid);
-  kt.template store_rows<DK>(Ks[0], tid);
-  vt.template store_rows<DK>(Vs[0], tid);
-
-  for (int t = 0; t < ntiles; ++t) {
+  const TileDma<D, DK> tdma(w, lane);
+  auto load_tile = [&](int n, const KVBuf& bb) {
+    tdma.load(K, p.ksn, n, N, bb.k, w);
+    tdma.load(V, p.vsn, n, N, bb.v, w);
+  };
+  // One key tile: computed from buffer bc while the next tile streams into buffer bn.
+  auto step = [&](int t, const KVBuf& bc, const KVBuf& bn) {
     const int n0 = t * BN;
-    const int cur = NBUF == 2 ? (t & 1) : 0;
+    wait_vmem();  // this wave's part of tile t is in LDS
     __syncthreads();
     const bool pre = t + 1 < ntiles;
-    if (pre) {
-      kt.load(K, p.ksn, n0 + BN, N, tid);
-      vt.load(V, p.vsn, n0 + BN, N, tid);
-    }
+    if (pre) load_tile(n0 + BN, bn);
     const int act = act_next;
     if (mrow && pre) act_next = mrow[t + 1];
     const bool work = has_rows && !(CAUSAL && n0 > qrow0 + 31) && act != 0;
     if (work) {
-      const bf16* Kc = Ks[cur];
-      const bf16* Vc = Vs[cur];
+      const bf16* Kc = bc.k;
+      const bf16* Vc = bc.v;
       const bool masked = (CAUSAL && n0 + BN - 1 > qrow0) || n0 + BN > N;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -747,12 +753,13 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
         adt[1] = mfma16x16x32(ones, pf[1], adt[1]);
       }
     }
-    if (pre) {
-      if (NBUF == 1) __syncthreads();
-      const int nxt = NBUF == 2 ? cur ^ 1 : 0;
-      kt.template store_rows<DK>(Ks[nxt], tid);
-      vt.template store_rows<DK>(Vs[nxt], tid);
-    }
+  };
+  for (int pass = 0;; ++pass) {
+  act_next = mrow ? mrow[0] : 1;
+  load_tile(0, buf0);
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, buf0, buf1);
+    if (t + 1 < ntiles) step(t + 1, buf1, buf0);
   }
   if (pass == 1) break;
 
@@ -872,13 +879,6 @@ __device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], c
       }
   }
 }
-
-// One LDS buffer of the dK/dV kernel: a query tile of Q and dO and its row-constant planes.
-struct QBuf {
-  bf16* q;
-  bf16* o;
-  float* rc;  // [planes][64 rows]
-};
 
 template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
