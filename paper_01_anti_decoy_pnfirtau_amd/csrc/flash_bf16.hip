@@ -209,10 +209,13 @@ struct KVBuf {
   bf16* v;
 };
 
-// One LDS buffer of the dK/dV kernel: a query tile of Q and dO and its row-constant planes.
+// One LDS buffer of the dK/dV kernel: a query tile of Q and dO, for D <= 64 also of their
+// row-scaled copies, and its row-constant planes.
 struct QBuf {
   bf16* q;
   bf16* o;
+  bf16* qx;
+  bf16* ox;
   float* rc;  // [planes][64 rows]
 };
 
@@ -614,6 +617,7 @@ __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2],
 // AGPRs) and no spills, which is far faster than spilling.
 template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdParams p) {
+  constexpr bool XT = D <= 64;  // writes the row-scaled Q and dO of the dK/dV kernel
   constexpr int BM = 128, BN = 64;
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
@@ -648,23 +652,30 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
   bf16x8 qf[2][KS], dof[2][KS];
   float rM[2], rG[2], rX[2];
   f32x4 dw_init[2];  // -D: the dW accumulator starts there
+  // D <= 64: the rows of Q and dO scaled by x = g/Z, for the dK/dV kernel (which runs next).
+  bf16* Qx = XT ? static_cast<bf16*>(p.qx) + (int64_t)bh * N * D : nullptr;
+  bf16* dOx = XT ? static_cast<bf16*>(p.dox) + (int64_t)bh * N * D : nullptr;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const int row = qrow0 + 16 * qb + r16;
+    const bool rok = row < N;
+    rM[qb] = rok ? rc_plane(p, bh, 0)[row] : 0.f;
+    const float nxd = rok ? rc_plane(p, bh, 1)[row] : 0.f;
+    rG[qb] = rok ? rc_plane(p, bh, 2)[row] : 0.f;
+    rX[qb] = rok ? rc_plane(p, bh, 3)[row] : 0.f;
+    dw_init[qb] = f32x4{nxd, nxd, nxd, nxd};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int col = 32 * ks + 8 * g;
-      const bool ok = row < N && col < D;
+      const bool ok = rok && col < D;
       qf[qb][ks] = ok ? ld16(Q + (int64_t)row * p.qsn + col) : zero_bf16x8();
       dof[qb][ks] = ok ? ld16(dO + (int64_t)row * p.dosn + col) : zero_bf16x8();
+      if (XT && ok) {
+        *reinterpret_cast<bf16x8*>(Qx + (int64_t)row * D + col) = scale_frag(qf[qb][ks], rX[qb]);
+        *reinterpret_cast<bf16x8*>(dOx + (int64_t)row * D + col) = scale_frag(dof[qb][ks], rX[qb]);
+      }
       if (PS) qf[qb][ks] = scale_frag(qf[qb][ks], scale);
     }
-    const bool ok = row < N;
-    rM[qb] = ok ? rc_plane(p, bh, 0)[row] : 0.f;
-    const float nxd = ok ? rc_plane(p, bh, 1)[row] : 0.f;
-    rG[qb] = ok ? rc_plane(p, bh, 2)[row] : 0.f;
-    rX[qb] = ok ? rc_plane(p, bh, 3)[row] : 0.f;
-    dw_init[qb] = f32x4{nxd, nxd, nxd, nxd};
   }
 
   const f32x4 s_init = PS ? f32x4{ntau, ntau, ntau, ntau} : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -774,7 +785,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
     c += __shfl_xor(c, 32, 64);
     const int qrow = qrow0 + 16 * qb + r16;
     if (g == 0 && qrow < N) {
-      rc_plane(p, bh, 7)[qrow] = c > 0 ? rG[qb] * (ds_mult * rX[qb]) / (float)c : 0.f;
+      // G''/Nmax for the dK/dV kernel with the row-scaled tiles (D <= 64), else G/Nmax
+      rc_plane(p, bh, 7)[qrow] = c > 0 ? (XT ? rG[qb] : rG[qb] * (ds_mult * rX[qb])) / (float)c : 0.f;
       double rs = (double)adt[qb][0];
       if (c > 1) rs -= (double)rG[qb] * (double)(c - 1);
       dsum += rs * (double)rX[qb];
@@ -880,8 +892,37 @@ __device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], c
   }
 }
 
+// D <= 64 form (Q and dO tiles also staged scaled by x = g/Z): the dV weight u^10 over s and
+// dS/(10 scale x) = u^9 dw + [u == M] G''/Nmax over dw = dW - D.  rc holds the planes
+// (M, -D, G''/Nmax).
+template <int KB>
+__device__ __forceinline__ void w_ds_qk_x(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const float* rc,
+                                          int pitch, int r4) {
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq) {
+    const f32x4 m4 = *reinterpret_cast<const f32x4*>(rc + r4 + 4 * qq);
+    const f32x4 t4 = *reinterpret_cast<const f32x4*>(rc + 2 * pitch + r4 + 4 * qq);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const float u = relu_mfma(s[qq][kb][i]);
+        const float u2 = u * u;
+        const float u4 = u2 * u2;
+        const float u9 = u4 * u4 * u;
+        s[qq][kb][i] = u9 * u;
+        const float tie = (u == m4[i]) ? t4[i] : 0.f;  // G'' = 0 on silent rows
+        dw[qq][kb][i] = __builtin_fmaf(u9, dw[qq][kb][i], tie);
+      }
+  }
+}
+
 template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
+  // D <= 64: the row factor x = g/Z rides on staged copies of Q and dO (written by the dQ
+  // kernel) for the dK and dV products, which saves two VALU ops per score; at D = 128 the
+  // extra tiles would not fit two workgroups per CU, and the rescaled form a = rho u is used.
+  constexpr bool XT = D <= 64;
   constexpr int KPW = DkdvCfg<D>::KPW, KB = DkdvCfg<D>::KB, BNK = DkdvCfg<D>::BNK;
   constexpr int BMQ = 64;
   constexpr int DK = D < 32 ? 32 : D;
@@ -893,14 +934,20 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   // (M, rho, kappa, -kappa D, G/Nmax) of the tile's rows: a lane reads the four consecutive
   // rows its registers cover as one f32x4 per plane (broadcast within a 16-lane group; the
   // four groups' rows are 8 apart, in different banks).
-  constexpr int NPL = 5;
+  // XT: three planes (M, -D, G''/Nmax).
+  constexpr int NPL = XT ? 3 : 5;
+  constexpr int XS = XT ? BMQ * DK : 8;  // scaled tiles (unused at D = 128)
   __shared__ __attribute__((aligned(16))) bf16 Qs0[BMQ * DK];
   __shared__ __attribute__((aligned(16))) bf16 dOs0[BMQ * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Qxs0[XS];
+  __shared__ __attribute__((aligned(16))) bf16 dOxs0[XS];
   __shared__ __attribute__((aligned(16))) float RC0[NPL * BMQ];
   __shared__ __attribute__((aligned(16))) bf16 Qs1[BMQ * DK];
   __shared__ __attribute__((aligned(16))) bf16 dOs1[BMQ * DK];
+  __shared__ __attribute__((aligned(16))) bf16 Qxs1[XS];
+  __shared__ __attribute__((aligned(16))) bf16 dOxs1[XS];
   __shared__ __attribute__((aligned(16))) float RC1[NPL * BMQ];
-  const QBuf buf0{Qs0, dOs0, RC0}, buf1{Qs1, dOs1, RC1};
+  const QBuf buf0{Qs0, dOs0, Qxs0, dOxs0, RC0}, buf1{Qs1, dOs1, Qxs1, dOxs1, RC1};
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
@@ -912,15 +959,19 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const bf16* K = static_cast<const bf16*>(p.k) + b * p.ksb + h * p.ksh;
   const bf16* V = static_cast<const bf16*>(p.v) + b * p.vsb + h * p.vsh;
   const bf16* dO = static_cast<const bf16*>(p.dout) + b * p.dosb + h * p.dosh;
-  // Staging of the row constants (planes 0, 4, 5, 6, 7 of the workspace: M, rho, kappa,
-  // -kappa D, G/Nmax): wave w copies plane w of the tile's rows, wave 0 also the last.
-  const float* RCgw = rc_plane(p, bh, w == 0 ? 0 : 3 + w);
+  // Staging of the row constants: wave w copies plane w of the tile's rows (XT: workspace
+  // planes 0, 1, 7 = M, -D, G''/Nmax; else 0, 4, 5, 6, 7 = M, rho, kappa, -kappa D, G/Nmax,
+  // wave 0 also the last).
+  const float* RCgw = rc_plane(p, bh, XT ? (w == 2 ? 7 : w) : (w == 0 ? 0 : 3 + w));
   const float* RCg4 = rc_plane(p, bh, 7);
+  const bf16* Qx = XT ? static_cast<const bf16*>(p.qx) + (int64_t)bh * N * D : nullptr;
+  const bf16* dOx = XT ? static_cast<const bf16*>(p.dox) + (int64_t)bh * N * D : nullptr;
   const int kv0 = kvb * BNK;
   const int kw0 = kv0 + KPW * w;
   const bool has_keys = kw0 < N;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
+  const float ds_mult = 10.f * scale;  // XT: the score loops form dS/(10 scale x)
   const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
 
   bf16x8 kf[KB][KS], vf[KB][KS];
@@ -957,9 +1008,13 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   auto load_tile = [&](int m, const QBuf& bb) {
     tdma.load(Q, p.qsn, m, N, bb.q, w);
     tdma.load(dO, p.dosn, m, N, bb.o, w);
+    if (XT) {
+      tdma.load(Qx, D, m, N, bb.qx, w);
+      tdma.load(dOx, D, m, N, bb.ox, w);
+    }
     const int row = min(m + lane, N - 1);
-    lds_dma4(RCgw + row, bb.rc + w * BMQ);
-    if (w == 0) lds_dma4(RCg4 + row, bb.rc + (NPL - 1) * BMQ);
+    if (w < NPL) lds_dma4(RCgw + row, bb.rc + w * BMQ);
+    if (!XT && w == 0) lds_dma4(RCg4 + row, bb.rc + (NPL - 1) * BMQ);
   };
   if (qt0 < nqt) load_tile(qt0 * BMQ, buf0);
 
@@ -986,6 +1041,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     if (work) {
       const bf16* Qc = bc.q;
       const bf16* dOc = bc.o;
+      const bf16* Qt = XT ? bc.qx : Qc;    // operand of dK += dS^T Q
+      const bf16* dOt = XT ? bc.ox : dOc;  // operand of dV += w^T dO
       const bool masked = (CAUSAL && m0 < kw0 + KPW - 1) || m0 + BMQ > N || kw0 + KPW > N;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -993,6 +1050,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         f32x4 s[2][KB], dw[2][KB];
 #pragma unroll
         for (int qq = 0; qq < 2; ++qq) {
+          // XT: the dW accumulator starts at -D of the four rows the lane's registers cover
+          const f32x4 dw0 = XT ? *reinterpret_cast<const f32x4*>(bc.rc + BMQ + 32 * hf + 8 * g + 4 * qq)
+                               : f32x4{0.f, 0.f, 0.f, 0.f};
           bf16x8 qa[KS], da[KS];
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
@@ -1002,7 +1062,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
           }
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
-            f32x4 a4 = s_init, c4 = {0.f, 0.f, 0.f, 0.f};
+            f32x4 a4 = s_init, c4 = dw0;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
               a4 = mfma16x16x32(qa[ks], kf[kb][ks], a4);
@@ -1015,7 +1075,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         affine_qk<KB, PS>(s, scale, ntau);
         if (masked) mask_qk<KB>(s, m0, hf, kw0, N, CAUSAL, g, r16);
         // rows 32 hf + 8 g + 4 qq + (0..3) of the tile are perm_row(2 hf + qq, 4 g + i)
-        w_ds_qk<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
+        if constexpr (XT) w_ds_qk_x<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
+        else w_ds_qk<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
         bf16x8 wf[KB], sf[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
@@ -1026,8 +1087,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         }
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const bf16x8 ot = tr_frag<DK>(dOc, flt, hf, db);
-          const bf16x8 qt_ = tr_frag<DK>(Qc, flt, hf, db);
+          const bf16x8 ot = tr_frag<DK>(dOt, flt, hf, db);
+          const bf16x8 qt_ = tr_frag<DK>(Qt, flt, hf, db);
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
             adv[db][kb] = mfma16x16x32(ot, wf[kb], adv[db][kb]);
@@ -1053,7 +1114,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         bf16x4 k4, v4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          k4[i] = (bf16)adk[db][kb][i];
+          k4[i] = (bf16)(XT ? adk[db][kb][i] * ds_mult : adk[db][kb][i]);
           v4[i] = (bf16)adv[db][kb][i];
         }
         *reinterpret_cast<bf16x4*>(dK + (int64_t)key * p.dksn + 16 * db + 4 * g) = k4;

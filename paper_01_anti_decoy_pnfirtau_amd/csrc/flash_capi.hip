@@ -61,8 +61,7 @@ extern "C" int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t q
 }
 
 extern "C" int64_t pnfx_flash_bwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D) {
-  (void)D;
-  return BwdWorkspace(B, H, N).total();
+  return BwdWorkspace(B, H, N, D).total();
 }
 
 extern "C" int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
@@ -92,7 +91,7 @@ extern "C" int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int
   PNFX_REQUIRE(M && Z && tau && dtau, "flash_bwd: null statistics / tau pointer");
   PNFX_REQUIRE(!o_lo || (dtype == PNFX_BF16 && aligned16(o_lo)),
                "flash_bwd: o_lo is a 16-byte aligned bf16 buffer with o's strides");
-  const BwdWorkspace wl(B, H, N);
+  const BwdWorkspace wl(B, H, N, D);
   PNFX_REQUIRE(workspace && workspace_bytes >= wl.total() &&
                    (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
                "flash_bwd: workspace needs %lld bytes, 256-byte aligned (got %lld)",
@@ -100,10 +99,12 @@ extern "C" int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int
   char* ws = static_cast<char*>(workspace);
   float* rcbuf = reinterpret_cast<float*>(ws);
   double* parts = reinterpret_cast<double*>(ws + wl.rc_bytes);
+  void* qx = wl.xt_bytes ? ws + wl.rc_bytes + wl.parts_bytes : nullptr;
+  void* dox = wl.xt_bytes ? ws + wl.rc_bytes + wl.parts_bytes + wl.xt_bytes : nullptr;
   BwdParams bp{q, k, v, o, o_lo, dout, dq, dk, dv,
                qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn, dosb, dosh, dosn,
                dqsb, dqsh, dqsn, dksb, dksh, dksn, dvsb, dvsh, dvsn,
-               M, Z, tile_mask, rcbuf, parts, dtau,
+               M, Z, tile_mask, rcbuf, parts, qx, dox, dtau,
                (int)B, (int)H, (int)N, (int)((N + 31) / 32), (int)((N + 63) / 64),
                bwd_nkvb(N, D), tau, scale, gamma};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
