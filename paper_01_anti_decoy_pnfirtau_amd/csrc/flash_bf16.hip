@@ -180,7 +180,8 @@ struct TileDma {
   static constexpr int CPR = DK / 8;      // 16-byte chunks per tile row
   static constexpr int NI = 64 * CPR / 256;  // loads per thread
   int row[NI], col[NI];
-  __device__ __forceinline__ TileDma(int w, int lane) {
+  unsigned off[NI];  // byte offset of the lane's chunks from the tile's first row
+  __device__ __forceinline__ TileDma(int w, int lane, int64_t sn) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       const int L = (4 * j + w) * 64 + lane;  // chunk index in the tile
@@ -188,10 +189,26 @@ struct TileDma {
       const int ch = pos ^ swz_rt<DK>(slot);
       row[j] = row_of_slot(slot);
       col[j] = 8 * (ch % (D / 8));
+      off[j] = (unsigned)(2 * (row[j] * sn + col[j]));
     }
   }
+  // A whole tile (row0 + 64 <= N) is a wave-uniform base plus 32-bit lane offsets, which the
+  // load takes as scalar base + vector offset: no per-load address arithmetic.
   __device__ __forceinline__ void load(const bf16* src, int64_t sn, int row0, int N, bf16* tile,
                                        int w) const {
+    if (row0 + 64 <= N) {
+      const char* base = reinterpret_cast<const char*>(src + (int64_t)row0 * sn);
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+        lds_dma16(reinterpret_cast<const bf16*>(base + off[j]), tile + (4 * j + w) * 512);
+    } else {
+      load_clamped(src, sn, row0, N, tile, w);
+    }
+  }
+  // Any tile, from the row and column alone (fewer registers held across the loop, more
+  // address arithmetic per load).
+  __device__ __forceinline__ void load_clamped(const bf16* src, int64_t sn, int row0, int N,
+                                               bf16* tile, int w) const {
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       const int r = min(row0 + row[j], N - 1);
@@ -393,10 +410,10 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
 
   // Software pipeline: tile t+1 streams from HBM/L2 straight into one LDS buffer while tile
   // t is computed from the other; one barrier per tile.
-  const TileDma<D, DK> tdma(w, lane);
+  const TileDma<D, DK> kdma(w, lane, p.ksn), vdma(w, lane, p.vsn);
   auto load_tile = [&](int n, const KVBuf& bb) {
-    tdma.load(K, p.ksn, n, N, bb.k, w);
-    tdma.load(V, p.vsn, n, N, bb.v, w);
+    kdma.load(K, p.ksn, n, N, bb.k, w);
+    vdma.load(V, p.vsn, n, N, bb.v, w);
   };
   auto step = [&](int t, const KVBuf& bc, const KVBuf& bn) {
     const int n0 = t * BN;
@@ -702,10 +719,10 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
   // byte until it is tested, so that its wait does not also wait for the tile prefetch.
   int act_next;
 
-  const TileDma<D, DK> tdma(w, lane);
+  const TileDma<D, DK> kdma(w, lane, p.ksn), vdma(w, lane, p.vsn);
   auto load_tile = [&](int n, const KVBuf& bb) {
-    tdma.load(K, p.ksn, n, N, bb.k, w);
-    tdma.load(V, p.vsn, n, N, bb.v, w);
+    kdma.load(K, p.ksn, n, N, bb.k, w);
+    vdma.load(V, p.vsn, n, N, bb.v, w);
   };
   // One key tile: computed from buffer bc while the next tile streams into buffer bn.
   auto step = [&](int t, const KVBuf& bc, const KVBuf& bn) {
@@ -1004,13 +1021,14 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
 
   // Tiles go straight from global memory to LDS buffer bb; rows >= N repeat row N - 1 (their
   // scores are masked), including their row constants.
-  const TileDma<D, DK> tdma(w, lane);
+  // (The register-lean clamped loads: this kernel is at the register limit.)
+  const TileDma<D, DK> tdma(w, lane, 0);
   auto load_tile = [&](int m, const QBuf& bb) {
-    tdma.load(Q, p.qsn, m, N, bb.q, w);
-    tdma.load(dO, p.dosn, m, N, bb.o, w);
+    tdma.load_clamped(Q, p.qsn, m, N, bb.q, w);
+    tdma.load_clamped(dO, p.dosn, m, N, bb.o, w);
     if (XT) {
-      tdma.load(Qx, D, m, N, bb.qx, w);
-      tdma.load(dOx, D, m, N, bb.ox, w);
+      tdma.load_clamped(Qx, D, m, N, bb.qx, w);
+      tdma.load_clamped(dOx, D, m, N, bb.ox, w);
     }
     const int row = min(m + lane, N - 1);
     if (w < NPL) lds_dma4(RCgw + row, bb.rc + w * BMQ);
