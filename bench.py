@@ -233,6 +233,99 @@ def profiled_traffic(kernel):
     return None
 
 
+C3 = dict(n_layers=6, d_model=256, n_heads=4, d_ff=1024, seq=512, batch=32, vocab=33278)
+
+
+def zipf_tokens(batch, seq, vocab, seed, s=1.1):
+    """Token ids ~ Zipf(s) truncated to [0, vocab) (rejection), seeded on the CPU."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    need, out = batch * seq, []
+    while need > 0:
+        z = rng.zipf(s, size=2 * need) - 1
+        z = z[z < vocab][:need]
+        out.append(z)
+        need -= len(z)
+    return torch.from_numpy(np.concatenate(out).reshape(batch, seq).astype(np.int64))
+
+
+def bench_lm(dev, steps=10, warmup=3):
+    """C3: one training step of the 6-layer LM with flash pn_fir_tau attention (bf16 autocast,
+    AdamW), eager and captured as one HIP graph.  Synthetic Zipf tokens, random init, dropout 0."""
+    from paper_01_anti_decoy_pnfirtau_amd.wikilm import (GraphedStep, WikiLM, WikiLMConfig,
+                                                          make_optimizer, train_step)
+
+    cfg = WikiLMConfig(d_model=C3["d_model"], n_heads=C3["n_heads"], n_layers=C3["n_layers"],
+                       d_ff=C3["d_ff"], max_seq=C3["seq"], dropout=0.0)
+    x = zipf_tokens(C3["batch"], C3["seq"], C3["vocab"], 0).to(dev)
+    out = {"config": C3, "data": "synthetic Zipf(1.1) tokens, random init, dropout 0"}
+    torch.manual_seed(0)
+    model = WikiLM(C3["vocab"], cfg, "pn_fir_tau_flash").to(dev)
+    opt = make_optimizer(model, cfg)
+    wall, _ = time_steps(lambda: train_step(model, opt, x), steps, warmup)
+    out["eager_ms_per_step"] = round(wall, 3)
+    torch.manual_seed(0)
+    model = WikiLM(C3["vocab"], cfg, "pn_fir_tau_flash").to(dev)
+    opt = make_optimizer(model, cfg, capturable=True)
+    g = GraphedStep(model, opt, x.clone())
+    wall_g, _ = time_steps(g.replay, steps, warmup)
+    out["graph_ms_per_step"] = round(wall_g, 3)
+    out["loss_after"] = round(float(g.loss), 4)
+    del g, model, opt
+    return out
+
+
+MHA6 = dict(n_layers=6, d_model=64, n_heads=4, N=1024, B=16)
+
+
+def bench_mha6(dev, steps=60, warmup=10):
+    """The reference's graph experiment (experiments/exp4c_cuda_graphs.py:75-108): a residual
+    stack of 6 PnFirTauFlashMHA layers (d_model 64, 4 heads, N 1024, B 16, bf16 autocast),
+    one forward+backward per step, eager and replayed from one HIP graph, at tau = -0.5 (all
+    tiles active) and +2.5 (all tiles silent)."""
+    from paper_01_anti_decoy_pnfirtau_amd import PnFirConfig, PnFirTauFlashMHA
+
+    torch.manual_seed(42)
+    acfg = PnFirConfig(d_model=MHA6["d_model"], n_heads=MHA6["n_heads"])
+    layers = torch.nn.ModuleList([PnFirTauFlashMHA(acfg) for _ in range(MHA6["n_layers"])]).to(dev)
+    x = torch.randn(MHA6["B"], MHA6["N"], MHA6["d_model"], device=dev, dtype=torch.bfloat16,
+                    requires_grad=True)
+    dy = torch.randn_like(x)
+
+    def step():
+        for prm in layers.parameters():
+            if prm.grad is not None:
+                prm.grad.zero_()
+        if x.grad is not None:
+            x.grad.zero_()
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            h = x
+            for lyr in layers:
+                h = h + lyr(h)
+        h.backward(dy)
+
+    out = {"config": MHA6}
+    for tau in (-0.5, 2.5):
+        with torch.no_grad():
+            for lyr in layers:
+                lyr.score_tau.fill_(tau)
+        eager, _ = time_steps(step, steps, warmup)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        graph, _ = time_steps(g.replay, steps, warmup)
+        out[f"tau={tau}"] = {"eager_ms_per_step": round(eager, 3), "graph_ms_per_step": round(graph, 3)}
+        del g
+    return out
+
+
 def cpu_baseline(slices=8):
     """numpy oracle (float32) forward + backward on `slices` (b, h) slices of C4."""
     import numpy as np
@@ -261,7 +354,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["flash", "fir", "copy"], default=None)
+    ap.add_argument("--only", choices=["flash", "fir", "copy", "lm", "mha6"], default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -276,6 +369,12 @@ def main():
         return
     if args.only == "fir":
         print(json.dumps(bench_fir(dev, reps=100)))
+        return
+    if args.only == "lm":
+        print(json.dumps(bench_lm(dev)))
+        return
+    if args.only == "mha6":
+        print(json.dumps(bench_mha6(dev)))
         return
 
     B, H, N, D = C4["B"], C4["H"], C4["N"], C4["D"]
@@ -306,6 +405,9 @@ def main():
     flops5 = 7 * gemm_flops(B5, H5, N5, D5)
     kern5 = kernel_times(q5, k5, v5, dO5, 0.0, max(3, args.steps // 4))
     del q5, k5, v5, dO5
+
+    lm = bench_lm(dev)
+    mha6 = bench_mha6(dev)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
@@ -340,6 +442,8 @@ def main():
         "wide_head": {"config": C5, "ms_per_step": round(wall5, 4),
                       "tflops": round(flops5 / (wall5 * 1e-3) / 1e12, 2),
                       "kernel_ms": {n: r["ms"] for n, r in kern5.items()}},
+        "lm_step": lm,
+        "mha6_stack": mha6,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -148,3 +148,35 @@ def test_hip_ops_refuse_cpu_tensors():
         torch.ops.pnfx.flash_fwd(q, q, q, torch.tensor(0.0), 0.25, 0.5, True, True, False, False)
     with pytest.raises(RuntimeError):
         P.flash_pn_fir_tau_attention(q, q, q, torch.tensor(0.0))
+
+
+def test_wikilm_variants_share_init_and_train_on_cpu():
+    """The LM consumer (experiments/exp4_wikitext2_lm.py:183-247) builds the same weights for
+    every attention variant from one seed and ties the head to the embedding.  Off-GPU the
+    row-fused variant takes the eager path, so its training steps agree exactly with the eager
+    model's; the flash variant has no CPU route (as in the reference) and raises."""
+    from paper_01_anti_decoy_pnfirtau_amd.wikilm import WikiLM, WikiLMConfig, make_optimizer, train_step
+
+    cfg = WikiLMConfig(d_model=32, n_heads=4, n_layers=2, d_ff=64, max_seq=32, dropout=0.0)
+    x = torch.randint(0, 50, (2, 32), generator=torch.Generator().manual_seed(0))
+    losses, states = {}, {}
+    for variant in ("pn_fir_tau", "pn_fir_tau_triton", "pn_fir_tau_flash"):
+        torch.manual_seed(0)
+        m = WikiLM(50, cfg, variant)
+        assert m.head.weight is m.embed.weight
+        states[variant] = {k: v.clone() for k, v in m.state_dict().items()}
+        opt = make_optimizer(m, cfg)
+        if variant == "pn_fir_tau_flash":
+            with pytest.raises(RuntimeError, match="GPU only"):
+                train_step(m, opt, x, amp=False)
+            continue
+        losses[variant] = [float(train_step(m, opt, x, amp=False)) for _ in range(2)]
+    ref = states["pn_fir_tau"]
+    for variant, st in states.items():
+        assert st.keys() == ref.keys()
+        for k in ref:
+            assert torch.equal(st[k], ref[k]), (variant, k)
+    assert losses["pn_fir_tau_triton"] == losses["pn_fir_tau"]
+    assert losses["pn_fir_tau"][1] < losses["pn_fir_tau"][0]
+    with pytest.raises(ValueError):
+        WikiLM(50, cfg, "softmax")
