@@ -401,7 +401,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["flash", "fir", "copy", "lm", "mha6", "ref"], default=None)
+    ap.add_argument("--only", choices=["flash", "fir", "copy", "lm", "mha6", "ref", "kernels"],
+                    default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -425,6 +426,14 @@ def main():
         return
     if args.only == "ref":
         print(json.dumps(bench_reference_configs(dev)))
+        return
+    if args.only == "kernels":  # per-stage HIP-event times at C4 and C5
+        out = {}
+        for name, c, std in (("C4", C4, 1.0), ("C5", C5, C5["D"] ** -0.25)):
+            q, k, v, dO = make_inputs(c["B"], c["H"], c["N"], c["D"], 0, dev, std=std)
+            out[name] = {n: r["ms"] for n, r in kernel_times(q, k, v, dO, 0.0, args.steps).items()}
+            del q, k, v, dO
+        print(json.dumps(out))
         return
 
     B, H, N, D = C4["B"], C4["H"], C4["N"], C4["D"]
