@@ -182,3 +182,66 @@ def test_flash_strided_inputs_match_contiguous(dev):
     o1 = flash_pn_fir_tau_attention(q, k, v, tau)
     o2 = flash_pn_fir_tau_attention(q.contiguous(), k.contiguous(), v.contiguous(), tau)
     assert torch.equal(o1, o2)
+
+
+FULL = [
+    # name, B, H, N, D, input std, checked (b, h) slice
+    ("C4", 4, 16, 8192, 64, 1.0, (2, 5)),
+    ("C5", 8, 8, 4096, 128, 128 ** -0.25, (7, 3)),
+]
+
+
+@pytest.mark.parametrize("name,B,H,N,D,std,bh", FULL)
+def test_flash_full_size_slice_matches_oracle(dev, name, B, H, N, D, std, bh):
+    """At the benchmark shapes: the whole batch runs on the GPU; one (b, h) slice of O, dQ, dK
+    and dV is checked against the float64 oracle on the same bf16 inputs (the slices are
+    independent, so one slice exercises every tile position of the full-size launch)."""
+    print(f"[flash full {name} B={B} H={H} N={N} D={D}]", flush=True)
+    g = torch.Generator().manual_seed(11)
+    q, k, v, dO = [(torch.randn(B, H, N, D, generator=g) * std).to(torch.bfloat16).to(dev)
+                   for _ in range(4)]
+    o, dq, dk, dv, _ = _run(q, k, v, 0.0, dO, None, 0.5, True)
+    b, h = bh
+    scale = 1.0 / np.sqrt(D)
+    Of, _, _, _, rq, rk, rv, _, _ = flash_oracle(q[b, h], k[b, h], v[b, h], 0.0, dO[b, h], scale,
+                                                 0.5, True)
+    for what, got, want in (("O", o, Of), ("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
+        assert_bf16_close(to_np64(got[b, h]), want, f"{name} {what}")
+
+
+def test_flash_full_size_gradients_scale_exactly_with_dout(dev):
+    """Size-independent property at C4: the backward is linear in dO and every operation in
+    it commutes with a power-of-two scale, so doubling dO doubles dQ, dK, dV and dtau
+    bit for bit (this also catches any read of uninitialised or racing memory)."""
+    print("[flash full C4 homogeneity]", flush=True)
+    B, H, N, D = 4, 16, 8192, 64
+    g = torch.Generator().manual_seed(12)
+    q, k, v, dO = [torch.randn(B, H, N, D, generator=g).to(torch.bfloat16).to(dev) for _ in range(4)]
+    _, dq1, dk1, dv1, dt1 = _run(q, k, v, 0.0, dO, None, 0.5, True)
+    _, dq2, dk2, dv2, dt2 = _run(q, k, v, 0.0, 2 * dO, None, 0.5, True)
+    for what, a, b2 in (("dQ", dq1, dq2), ("dK", dk1, dk2), ("dV", dv1, dv2)):
+        assert torch.equal(2 * a, b2), what
+    assert float(2 * dt1) == float(dt2)
+
+
+def test_flash_full_size_planted_tile_mask(dev):
+    """The benchmark's 50 %-silent configuration at full C4 size: with key blocks
+    {even j} \\ {96} zeroed and tau = 0.25, the forward's 64x64 activity map equals the
+    oracle's for a checked slice, and exactly 4128 of the 8256 causal tiles of every slice are
+    silent."""
+    print("[flash full C4 planted mask]", flush=True)
+    B, H, N, D = 4, 16, 8192, 64
+    g = torch.Generator().manual_seed(13)
+    q, k, v = [torch.randn(B, H, N, D, generator=g).to(torch.bfloat16).to(dev) for _ in range(3)]
+    nb = N // 64
+    silent = [j for j in range(nb) if j % 2 == 0 and j != 96]
+    for j in silent:
+        k[:, :, 64 * j:64 * j + 64] = 0
+    o, M, Z, Nm, mask = flash_pn_fir_tau_attention_with_stats(q, k, v, torch.tensor(0.25, device=dev))
+    m64 = tile_mask_64(mask).cpu().numpy().reshape(B, H, nb, nb).astype(bool)
+    causal = np.tril(np.ones((nb, nb), dtype=bool))
+    assert not (m64 & ~causal).any()
+    assert ((~m64) & causal).sum(axis=(2, 3)).tolist() == [[4128] * H] * B
+    act, amb = O.tile_activity(to_np64(q[1, 7]), to_np64(k[1, 7]), 0.25)
+    assert not amb.any()
+    assert np.array_equal(m64[1, 7], act)
