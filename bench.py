@@ -429,9 +429,13 @@ def main():
         return
     if args.only == "kernels":  # per-stage HIP-event times at C4 and C5
         out = {}
-        for name, c, std in (("C4", C4, 1.0), ("C5", C5, C5["D"] ** -0.25)):
+        for name, c, std in (("C4", C4, 1.0), ("C4_silent50", C4, 1.0), ("C5", C5, C5["D"] ** -0.25)):
             q, k, v, dO = make_inputs(c["B"], c["H"], c["N"], c["D"], 0, dev, std=std)
-            out[name] = {n: r["ms"] for n, r in kernel_times(q, k, v, dO, 0.0, args.steps).items()}
+            tau = 0.0
+            if name == "C4_silent50":
+                plant_silent(k, c["N"])
+                tau = 0.25
+            out[name] = {n: r["ms"] for n, r in kernel_times(q, k, v, dO, tau, args.steps).items()}
             del q, k, v, dO
         print(json.dumps(out))
         return
