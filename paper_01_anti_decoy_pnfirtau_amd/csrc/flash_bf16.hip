@@ -11,17 +11,17 @@
 // K Q^T, whose C layout gives each lane one query row (lane % 16) and four keys per 16-key
 // block.  The key order of the K fragment is permuted (perm_row below) so that the 8 keys a
 // lane group holds after two blocks are contiguous: the C registers then feed the next
-// MFMA (P^T or dS^T as its B operand) directly, and the A operand (V^T or K^T) is one
-// 16-byte LDS read from a transposed tile.  The dK/dV kernel computes S = Q K^T with the
+// MFMA (P^T or dS^T as its B operand) directly, and the A operand (V^T or K^T) comes from
+// the row-major tile through two transposing LDS reads.  The dK/dV kernel computes S = Q K^T with the
 // same trick on the query axis.  MFMA results are bitwise transpose-symmetric on gfx950,
 // so every kernel recomputes exactly the forward's scores; the peak-tie test u == M of
 // the backward therefore sees the forward's ties.
 //
-// Backward (deterministic, no atomics): a per-row preprocess kernel forms the row
-// constants (D_i = <dO_i, O_i>/g_i and the gate/normaliser factors); a key-parallel
-// kernel accumulates dK and dV; a query-parallel kernel accumulates dQ and the tau
-// partials; a one-block kernel sums the partials in fp64.  Both backward kernels skip the 32x64
-// sub-tiles that the forward recorded as silent.
+// Backward (deterministic, no atomics), in this order: a per-row preprocess kernel forms the
+// row constants (D_i = <dO_i, O_i>/g_i and the gate/normaliser factors); a query-parallel
+// kernel accumulates dQ and the tau partials and counts the peak ties; a one-block kernel
+// sums the partials in fp64; a key-parallel kernel accumulates dK and dV.  Both gradient
+// kernels skip the 32x64 sub-tiles that the forward recorded as silent.
 #include <cmath>
 
 #include "flash.h"
@@ -117,46 +117,6 @@ __device__ __forceinline__ bf16x8 tr_frag(const bf16* tile, const FragLane& fl, 
   return __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// Register-staged copy of rows [row0, row0 + ROWS) of an [N, D] bf16 slice (row stride sn).
-// Chunk c of a thread covers rows 2*(c / CPR) and 2*(c / CPR) + 1 at columns
-// 8*(c % CPR) .. +7 (CPR = D/8 chunks per row), so a wave's load instruction reads whole
-// contiguous rows.  load() issues the global reads into registers (rows >= N read as zero);
-// store_rows() writes them to a row-major tile.
-template <int ROWS, int D>
-struct PairTile {
-  static constexpr int CPR = D / 8;
-  static constexpr int NCH = (ROWS / 2) * CPR;
-  static constexpr int PER = (NCH + 255) / 256;
-  static_assert(ROWS == 64, "tiles are 64 rows (the slot_of permutation)");
-  u32x4 a[PER], b[PER];
-
-  __device__ __forceinline__ void load(const bf16* src, int64_t sn, int row0, int N, int tid) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = tid + 256 * i;
-      a[i] = u32x4{0u, 0u, 0u, 0u};
-      b[i] = u32x4{0u, 0u, 0u, 0u};
-      if (NCH % 256 == 0 || c < NCH) {
-        const int r = row0 + 2 * (c / CPR), col = 8 * (c % CPR);
-        if (r < N) a[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)r * sn + col);
-        if (r + 1 < N) b[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(r + 1) * sn + col);
-      }
-    }
-  }
-  template <int DK>
-  __device__ __forceinline__ void store_rows(bf16* dst, int tid) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = tid + 256 * i;
-      if (NCH % 256 == 0 || c < NCH) {
-        const int r = 2 * (c / CPR), ch = c % CPR;
-        *reinterpret_cast<u32x4*>(dst + rt_off<DK>(r, ch)) = a[i];
-        *reinterpret_cast<u32x4*>(dst + rt_off<DK>(r + 1, ch)) = b[i];
-      }
-    }
-  }
-};
-
 // Direct global -> LDS staging of a 64-row tile (rows row0 .. row0 + 63 of an [N, D] bf16
 // slice with row stride sn) into the swizzled row-major layout, with global_load_lds_dwordx4:
 // no register staging and no LDS store instructions.  Each such load writes 16 bytes per
@@ -238,18 +198,6 @@ struct QBuf {
 
 // Wait for this wave's outstanding global loads (including direct-to-LDS ones).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// Zero the k-padding chunks [D/8, DK/8) of a row-major tile (the 32-wide MFMA when D < 32).
-template <int ROWS, int D, int DK>
-__device__ __forceinline__ void zero_pad_cols(bf16* dst, int tid) {
-  if (D < DK) {
-    constexpr int PC = (DK - D) / 8;
-    for (int c = tid; c < ROWS * PC; c += 256) {
-      const int r = c / PC, ch = D / 8 + c % PC;
-      *reinterpret_cast<u32x4*>(dst + rt_off<DK>(r, ch)) = u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-}
 
 // Multiply the 8 bf16 values of a fragment by an exact power of two (no rounding).
 __device__ __forceinline__ bf16x8 scale_frag(bf16x8 v, float s) {
@@ -839,9 +787,10 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
   }
 }
 
-// dK, dV and tau partials: key-parallel.  Each wave owns KPW keys (32 for D <= 64, 16 for
-// D = 128) held as MFMA B fragments; the workgroup streams 64-row query tiles (Q, dO and
-// their transposes, plus the row constants) through LDS from the causal diagonal down.
+// dK and dV: key-parallel.  Each wave owns KPW consecutive keys (32 for D <= 64, 16 for
+// D = 128) held as MFMA B fragments; the workgroup streams 64-row query tiles (Q and dO, for
+// D <= 64 also their row-scaled copies, plus the row constants) through LDS from the causal
+// diagonal down; the transposed operands come from the same tiles through transposing reads.
 template <int D>
 struct DkdvCfg {
   static constexpr int KPW = D <= 64 ? 32 : 16;
