@@ -202,6 +202,42 @@ def bench_fir(dev, reps=200, pairs=20):
             "same_bytes_copy_gbps": round(nbytes / (cus * 1e-6) / 1e9, 1)}
 
 
+def bench_rows(dev, reps=20):
+    """Row-fused score kernels (the materialised-score path, PnFirTauTritonMHA) on the C3
+    attention's score tensor [B=32, H=4, 512, 512] bf16, causal, p = 10: HBM GB/s of the
+    algorithmic bytes (forward reads the scores and writes the weights; backward reads the
+    scores and dW and writes dScores; the 12-byte row statistics are included)."""
+    from paper_01_anti_decoy_pnfirtau_amd import ops
+
+    g = torch.Generator().manual_seed(9)
+    raw = (torch.randn(32, 4, 512, 512, generator=g) * 2).to(torch.bfloat16).to(dev)
+    dw = torch.randn(32, 4, 512, 512, generator=g).to(torch.bfloat16).to(dev)
+    tau = torch.tensor(0.0, device=dev)
+    w, M, Z, Nm = ops.pn_rows_fwd(raw, tau, 1.0 / 8, 10.0, 0.5, True, True)
+
+    def fwd():
+        ops.pn_rows_fwd(raw, tau, 1.0 / 8, 10.0, 0.5, True, True)
+
+    def bwd():
+        ops.pn_rows_bwd(dw, raw, tau, M, Z, Nm, 1.0 / 8, 10.0, 0.5, True, True)
+
+    R, n = raw.numel() // 512, raw.numel()
+    out = {"shape": [32, 4, 512, 512]}
+    for name, fn, nbytes in (("fwd", fwd, 2 * n * 2 + R * 12), ("bwd", bwd, 3 * n * 2 + R * 16)):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        out[name] = {"us": round(us, 2), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+    return out
+
+
 def bench_copy(dev, mib=512, reps=20):
     """A plain device copy of known size: the calibration point for FETCH_SIZE / WRITE_SIZE."""
     a = torch.empty(mib << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -401,7 +437,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["flash", "fir", "copy", "lm", "mha6", "ref", "kernels"],
+    ap.add_argument("--only", choices=["flash", "fir", "copy", "lm", "mha6", "ref", "kernels",
+                                       "rows"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -426,6 +463,9 @@ def main():
         return
     if args.only == "ref":
         print(json.dumps(bench_reference_configs(dev)))
+        return
+    if args.only == "rows":
+        print(json.dumps(bench_rows(dev)))
         return
     if args.only == "kernels":  # per-stage HIP-event times at C4 and C5
         out = {}
@@ -472,6 +512,7 @@ def main():
     lm = bench_lm(dev)
     mha6 = bench_mha6(dev)
     refcfg = bench_reference_configs(dev)
+    rows = bench_rows(dev)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
@@ -509,6 +550,7 @@ def main():
         "lm_step": lm,
         "mha6_stack": mha6,
         "reference_configs": refcfg,
+        "row_kernels": rows,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
