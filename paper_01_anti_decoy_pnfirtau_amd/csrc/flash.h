@@ -31,6 +31,7 @@ struct BwdParams {
   float* rc;         // row constants [B*H*N][8], layout private to each dtype's kernels
   double* partials;  // tau partials, one per wave of the dq kernel (bf16: [B*H][N/128][4])
   void *qx, *dox;    // bf16, D <= 64: Q and dO rows scaled by g/Z, contiguous [B*H, N, D]
+  uint8_t* ktact;    // [B*H][nk64]: 64-key tiles with any active tile-mask entry (mask given)
   float* dtau;
   int B, H, N, nq32, nk64, nkvb;
   const float* tau;
@@ -44,16 +45,18 @@ inline int bwd_nkvb(int64_t N, int64_t D) {
 }
 // Workspace of the backward: row constants, tau partials (fp64, one per 32 query rows: the
 // bf16 dq kernel's waves; the fp32 kernels use one per 64 rows), and for D <= 64 the
-// row-scaled copies of Q and dO that the bf16 dK/dV kernel reads.
+// row-scaled copies of Q and dO that the bf16 dK/dV kernel reads, and one activity byte per
+// 64-key tile.
 struct BwdWorkspace {
-  int64_t rc_bytes, parts_bytes, xt_bytes;
+  int64_t rc_bytes, parts_bytes, xt_bytes, kt_bytes;
   BwdWorkspace(int64_t B, int64_t H, int64_t N, int64_t D) {
     const int64_t slots = B * H * ((N + 127) / 128) * 4;
     rc_bytes = round256(B * H * N * 8 * 4);
     parts_bytes = round256(slots * 8);
     xt_bytes = D <= 64 ? round256(B * H * N * D * 2) : 0;  // each of Qx, dOx
+    kt_bytes = round256(B * H * ((N + 63) / 64));
   }
-  int64_t total() const { return rc_bytes + parts_bytes + 2 * xt_bytes; }
+  int64_t total() const { return rc_bytes + parts_bytes + 2 * xt_bytes + kt_bytes; }
   static int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
 };
 

@@ -506,6 +506,11 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   const int64_t row = (int64_t)blockIdx.x * RPB + tid / LPR;
   const int part = tid % LPR;
   const int64_t total = (int64_t)p.B * p.H * p.N;
+  if (p.ktact) {  // cleared here, set by the dQ kernel, read by the dK/dV kernel
+    const int64_t nkt = (int64_t)p.B * p.H * p.nk64;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + tid; i < nkt; i += (int64_t)gridDim.x * 256)
+      p.ktact[i] = 0;
+  }
   float dot = 0.f;
   if (row < total) {
     const int64_t bh = row / p.N, i = row % p.N;
@@ -683,6 +688,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
     if (mrow && pre) act_next = mrow[t + 1];
     const bool work = has_rows && !(CAUSAL && n0 > qrow0 + 31) && act != 0;
     if (work) {
+      // key tile t has an active entry: the dK/dV kernel schedules it among the active tiles
+      if (mrow && lane == 0) p.ktact[(int64_t)bh * p.nk64 + t] = 1;
       const bf16* Kc = bc.k;
       const bf16* Vc = bc.v;
       const bool masked = (CAUSAL && n0 + BN - 1 > qrow0) || n0 + BN > N;
@@ -883,6 +890,32 @@ __device__ __forceinline__ void w_ds_qk_x(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB],
   }
 }
 
+// Position e of the key-tile order of one (b, h): the tiles with act[t] != 0 ascending, then
+// the others ascending.  Returns the tile (or -1 past the end) and whether it is active.
+// Wave-uniform; two sweeps of nk64 bytes with ballots.
+__device__ __forceinline__ int ordered_ktile(const uint8_t* act, int nk64, int e, int lane,
+                                             bool& active) {
+  int na = 0;
+  for (int c = 0; c < nk64; c += 64) {
+    const bool f = c + lane < nk64 && act[c + lane] != 0;
+    na += __popcll(__ballot(f));
+  }
+  active = e < na;
+  int want = active ? e : e - na;
+  for (int c = 0; c < nk64; c += 64) {
+    const bool f = c + lane < nk64 && (act[c + lane] != 0) == active;
+    const uint64_t bal = __ballot(f);
+    const int cnt = __popcll(bal);
+    if (want < cnt) {
+      const int below = __popcll(bal & ((1ull << lane) - 1ull));
+      return c + __ffsll((long long)__ballot(f && below == want)) - 1;
+    }
+    want -= cnt;
+  }
+  active = false;
+  return -1;
+}
+
 template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   // D <= 64: the row factor x = g/Z rides on staged copies of Q and dO (written by the dQ
@@ -932,9 +965,29 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const float* RCg4 = rc_plane(p, bh, 7);
   const bf16* Qx = XT ? static_cast<const bf16*>(p.qx) + (int64_t)bh * N * D : nullptr;
   const bf16* dOx = XT ? static_cast<const bf16*>(p.dox) + (int64_t)bh * N * D : nullptr;
-  const int kv0 = kvb * BNK;
-  const int kw0 = kv0 + KPW * w;
-  const bool has_keys = kw0 < N;
+  // The workgroup's 64-key tiles.  With the tile activity of the dQ stage, workgroup j of a
+  // (b, h) takes positions TPW j .. TPW j + TPW - 1 of the order "active tiles ascending, then
+  // silent tiles": active tiles share workgroups, so no wave idles beside an active one, and
+  // a workgroup of silent tiles only writes zeros.  Without it, tiles in index order.
+  constexpr int TPW = BNK / 64;
+  int wtile, tile0;
+  bool wact = true, wg_active = true;
+  if (p.ktact) {
+    const uint8_t* act = p.ktact + (int64_t)bh * p.nk64;
+    wtile = ordered_ktile(act, p.nk64, TPW * kvb + (KPW * w) / 64, lane, wact);
+    tile0 = ordered_ktile(act, p.nk64, TPW * kvb, lane, wg_active);
+    // wave-uniform by construction; keep them in scalar registers
+    wtile = __builtin_amdgcn_readfirstlane(wtile);
+    tile0 = __builtin_amdgcn_readfirstlane(tile0);
+    wact = __builtin_amdgcn_readfirstlane(wact ? 1 : 0) != 0;
+    wg_active = __builtin_amdgcn_readfirstlane(wg_active ? 1 : 0) != 0;
+  } else {
+    wtile = (kvb * BNK + KPW * w) / 64;
+    tile0 = kvb * TPW;
+  }
+  const int kw0 = wtile < 0 ? N : wtile * 64 + (KPW * w) % 64;
+  const bool has_keys = kw0 < N;  // the wave writes dK, dV rows (zeros if silent)
+  const bool live = has_keys && wact;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
   const float ds_mult = 10.f * scale;  // XT: the score loops form dS/(10 scale x)
@@ -964,9 +1017,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     }
 
   const int nqt = (N + BMQ - 1) / BMQ;
-  const int qt0 = CAUSAL ? kv0 / BMQ : 0;
-  const int ktile = kw0 >> 6;  // 64-key tile of this wave's keys (forward mask column)
-  const uint8_t* mcol = (p.mask && has_keys) ? p.mask + (int64_t)bh * p.nq32 * p.nk64 + ktile : nullptr;
+  // first query tile: the causal diagonal of the workgroup's lowest active tile (the first
+  // in the order); none if the workgroup has only silent tiles
+  const int qt0 = !wg_active ? nqt : (CAUSAL ? tile0 * 64 / BMQ : 0);
+  const uint8_t* mcol = (p.mask && live) ? p.mask + (int64_t)bh * p.nq32 * p.nk64 + wtile : nullptr;
 
   // Tiles go straight from global memory to LDS buffer bb; rows >= N repeat row N - 1 (their
   // scores are masked), including their row constants.
@@ -1004,7 +1058,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     if (pre) load_tile(m0 + BMQ, bn);
     const int act0 = act_next[0], act1 = act_next[1];
     if (mcol && pre) fetch_active(m0 + BMQ);
-    const bool work = has_keys && !(CAUSAL && m0 + BMQ - 1 < kw0) && (act0 | act1) != 0;
+    const bool work = live && !(CAUSAL && m0 + BMQ - 1 < kw0) && (act0 | act1) != 0;
     if (work) {
       const bf16* Qc = bc.q;
       const bf16* dOc = bc.o;

@@ -161,6 +161,49 @@ def test_flash_tile_mask_planted_silent_blocks(dev, dtype):
     assert (~act[0, 0]).sum() - (nb * nb - causal_tiles) == sum(nb - j for j in silent)
 
 
+# Key blocks zeroed at tau = 0.25 are silent for every query: the dK/dV stage then schedules
+# the active 64-key tiles first (two per workgroup at D <= 64) and gives the silent ones
+# workgroups of their own, which only write zeros.  Patterns: alternate blocks, an irregular
+# set with an odd tile count (the last workgroup holds one tile), every block but the last,
+# every block, and a non-causal case.
+SILENT_KEY_CASES = [
+    # N, D, causal, silent 64-key blocks
+    (512, 64, True, "even"),
+    (700, 64, True, "irregular"),
+    (640, 128, True, "even"),
+    (512, 64, False, "odd"),
+    (384, 16, True, "all_but_last"),
+    (256, 64, True, "all"),
+]
+
+
+@pytest.mark.parametrize("N,D,causal,pattern", SILENT_KEY_CASES)
+def test_flash_gradients_with_silent_key_tiles(dev, N, D, causal, pattern):
+    print(f"[flash silent key tiles N={N} D={D} causal={causal} {pattern}]", flush=True)
+    B, H = 1, 2
+    nb = (N + 63) // 64
+    blocks = {"even": [j for j in range(nb) if j % 2 == 0],
+              "odd": [j for j in range(nb) if j % 2 == 1],
+              "irregular": [0, 2, 3, 6, 7, 9],
+              "all_but_last": list(range(nb - 1)),
+              "all": list(range(nb))}[pattern]
+    q = seeded((B, H, N, D), 50, torch.bfloat16, dev)
+    k = seeded((B, H, N, D), 51, torch.bfloat16, dev)
+    v = seeded((B, H, N, D), 52, torch.bfloat16, dev)
+    dO = seeded((B, H, N, D), 53, torch.bfloat16, dev)
+    for j in blocks:
+        k[:, :, 64 * j:64 * j + 64] = 0
+    scale = 1.0 / np.sqrt(D)
+    o, dq, dk, dv, dtau = _run(q, k, v, 0.25, dO, scale, 0.5, causal)
+    Of, M, Z, Nm, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, 0.25, dO, scale, 0.5, causal)
+    for name, got, want in (("O", o, Of), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert_bf16_close(to_np64(got), want, name)
+    # silent key blocks get exactly zero dK and dV
+    for j in blocks:
+        assert torch.all(dk[:, :, 64 * j:64 * j + 64] == 0) and torch.all(dv[:, :, 64 * j:64 * j + 64] == 0)
+    assert_sum_close(float(dtau), rdt, dabs, BF16_ATOL, "dtau")
+
+
 def test_flash_backward_is_deterministic(dev):
     B, H, N, D = 2, 2, 512, 64
     q = seeded((B, H, N, D), 50, torch.bfloat16, dev)
