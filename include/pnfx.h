@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define PNFX_ABI_VERSION 2
+#define PNFX_ABI_VERSION 3
 
 #define PNFX_OK 0
 #define PNFX_EINVAL (-1)       /* bad shape / stride / alignment / argument */
@@ -109,16 +109,26 @@ int pnfx_pn_rows_bwd(const void* dw, int64_t dw_rs, const void* raw, int64_t raw
  *                1 where the 32-query x 64-key sub-tile has a positive
  *                rectified score (the skip rule of src/triton_pnfirtau.py:395-400
  *                at 32-row granularity; OR adjacent row pairs for the 64x64 view).
+ *   workspace  : optional (may be NULL), pnfx_flash_fwd_workspace_size(B, H, N, D)
+ *                bytes, 256-byte aligned.  With it (bf16, tau > 0) the forward first
+ *                takes the largest key norm of every 64-key tile and skips, without
+ *                forming their scores or loading their K/V, the tiles where
+ *                max|q| max|k| scale <= tau (Cauchy-Schwarz: every score is then
+ *                <= 0).  Results are identical with and without it.
  * D in {16, 32, 64, 128}.  Replaces _flash_pn_fir_tau_fwd_kernel
  * (src/triton_pnfirtau.py:313-443) through _FlashPnFirTauFn.forward (:816-898).
  */
 int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
                    int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
                    int64_t vsh, int64_t vsn, void* o, int64_t osb, int64_t osh, int64_t osn,
-                   void* o_lo, float* M, float* Z, int32_t* Nmax, uint8_t* tile_mask, int64_t B,
-                   int64_t H,
+                   void* o_lo, float* M, float* Z, int32_t* Nmax, uint8_t* tile_mask,
+                   void* workspace, int64_t workspace_bytes, int64_t B, int64_t H,
                    int64_t N, int64_t D, const float* tau, float scale, float gamma,
                    int has_gamma, int causal, int dtype, void* stream);
+
+/* Bytes of the optional pnfx_flash_fwd workspace for this shape (the per-tile key
+ * norms of its silent-tile bound).  No counterpart in the reference. */
+int64_t pnfx_flash_fwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D);
 
 /* Bytes of device workspace pnfx_flash_bwd needs for this shape. */
 int64_t pnfx_flash_bwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D);

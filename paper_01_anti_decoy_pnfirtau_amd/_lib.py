@@ -11,7 +11,7 @@ import os
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpnfx.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 PNFX_F32 = 0
 PNFX_BF16 = 1
 PNFX_BWD_PREPARE, PNFX_BWD_DKDV, PNFX_BWD_DQ, PNFX_BWD_ALL = 1, 2, 4, 7
@@ -37,7 +37,9 @@ def _declare(lib: ctypes.CDLL) -> None:
              i32, vp], i32),
         "pnfx_flash_fwd": (
             [vp, i64, i64, i64] * 4
-            + [vp, vp, vp, vp, vp, i64, i64, i64, i64, vp, f32, f32, i32, i32, i32, vp], i32),
+            + [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, f32, f32, i32, i32, i32, vp],
+            i32),
+        "pnfx_flash_fwd_workspace_size": ([i64, i64, i64, i64], i64),
         "pnfx_flash_bwd_workspace_size": ([i64, i64, i64, i64], i64),
         "pnfx_flash_bwd": (
             [vp, i64, i64, i64] * 4
@@ -80,6 +82,6 @@ def exported_symbols() -> list[str]:
     """Names of every entry point include/pnfx.h declares."""
     return [
         "pnfx_abi_version", "pnfx_last_error", "pnfx_fir_fwd", "pnfx_fir_bwd",
-        "pnfx_pn_rows_fwd", "pnfx_pn_rows_bwd", "pnfx_flash_fwd",
+        "pnfx_pn_rows_fwd", "pnfx_pn_rows_bwd", "pnfx_flash_fwd", "pnfx_flash_fwd_workspace_size",
         "pnfx_flash_bwd_workspace_size", "pnfx_flash_bwd", "pnfx_flash_bwd_stages",
     ]

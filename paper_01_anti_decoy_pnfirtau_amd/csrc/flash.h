@@ -14,6 +14,7 @@ struct FwdParams {
   float* Z;
   int32_t* Nmax;  // optional: the peak-tie counts are only formed when requested
   uint8_t* mask;
+  float* knorm;  // optional [B*H][nk64]: largest key norm per 64-key tile (silent-tile bound)
   int B, H, N, nq32, nk64;
   const float* tau;
   float scale, gamma;

@@ -34,11 +34,16 @@ int check_shape(int64_t B, int64_t H, int64_t N, int64_t D) {
 
 using namespace pnfx;
 
+extern "C" int64_t pnfx_flash_fwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D) {
+  (void)D;
+  return BwdWorkspace::round256(B * H * ((N + 63) / 64) * 4);
+}
+
 extern "C" int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
                               int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
                               int64_t vsh, int64_t vsn, void* o, int64_t osb, int64_t osh,
                               int64_t osn, void* o_lo, float* M, float* Z, int32_t* Nmax,
-                              uint8_t* tile_mask,
+                              uint8_t* tile_mask, void* workspace, int64_t workspace_bytes,
                               int64_t B, int64_t H, int64_t N, int64_t D, const float* tau,
                               float scale, float gamma, int has_gamma, int causal, int dtype,
                               void* stream) {
@@ -52,8 +57,13 @@ extern "C" int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t q
   PNFX_REQUIRE(M && Z && tau, "flash_fwd: null statistics / tau pointer");
   PNFX_REQUIRE(!o_lo || (dtype == PNFX_BF16 && aligned16(o_lo)),
                "flash_fwd: o_lo is a 16-byte aligned bf16 buffer with o's strides");
+  const int64_t fws = pnfx_flash_fwd_workspace_size(B, H, N, D);
+  PNFX_REQUIRE(!workspace || (workspace_bytes >= fws &&
+                              (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0),
+               "flash_fwd: workspace needs %lld bytes, 256-byte aligned (got %lld)",
+               (long long)fws, (long long)workspace_bytes);
   FwdParams fp{q, k, v, o, o_lo, qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn,
-               M, Z, Nmax, tile_mask, (int)B, (int)H, (int)N,
+               M, Z, Nmax, tile_mask, static_cast<float*>(workspace), (int)B, (int)H, (int)N,
                (int)((N + 31) / 32), (int)((N + 63) / 64), tau, scale, gamma, has_gamma != 0};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   return dtype == PNFX_BF16 ? flash_fwd_bf16(fp, D, causal != 0, st)

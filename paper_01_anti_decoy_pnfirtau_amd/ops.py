@@ -218,10 +218,13 @@ def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma:
     Nm = torch.empty((B, H, N) if with_nmax else (0,), device=q.device, dtype=torch.int32)
     mask = torch.empty((B * H, (N + 31) // 32, (N + 63) // 64), device=q.device, dtype=torch.uint8)
     t32 = _tau32(tau)
+    # workspace of the silent-tile bound (per-tile key norms; a few KiB)
+    nws = _lib.lib().pnfx_flash_fwd_workspace_size(B, H, N, D)
+    ws = torch.empty(nws, device=q.device, dtype=torch.uint8)
     rc = _lib.lib().pnfx_flash_fwd(
         *_ptr4(q), *_ptr4(k), *_ptr4(v), *_ptr4(o), o_lo.data_ptr() if bf else None,
         M.data_ptr(), Z.data_ptr(), Nm.data_ptr() if with_nmax else None, mask.data_ptr(),
-        B, H, N, D,
+        ws.data_ptr(), nws, B, H, N, D,
         t32.data_ptr(), scale, gamma, int(has_gamma), int(causal), code, _stream(q))
     _lib.check(rc, "pnfx_flash_fwd")
     return o, o_lo, M, Z, Nm, mask

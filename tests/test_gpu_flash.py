@@ -204,6 +204,77 @@ def test_flash_gradients_with_silent_key_tiles(dev, N, D, causal, pattern):
     assert_sum_close(float(dtau), rdt, dabs, BF16_ATOL, "dtau")
 
 
+def _fwd_abi(q, k, v, tau, scale, with_workspace):
+    """pnfx_flash_fwd called directly, with or without the silent-tile bound's workspace."""
+    from paper_01_anti_decoy_pnfirtau_amd import _lib
+    lib = _lib.lib()
+    B, H, N, D = q.shape
+    p4 = lambda t: (t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))  # noqa: E731
+    o, o_lo = torch.empty_like(q), torch.empty_like(q)
+    M = torch.empty((B, H, N), device=q.device)
+    Z = torch.empty_like(M)
+    Nm = torch.empty((B, H, N), device=q.device, dtype=torch.int32)
+    mask = torch.empty((B * H, (N + 31) // 32, (N + 63) // 64), device=q.device, dtype=torch.uint8)
+    nws = lib.pnfx_flash_fwd_workspace_size(B, H, N, D)
+    ws = torch.empty(nws, device=q.device, dtype=torch.uint8) if with_workspace else None
+    t32 = torch.tensor([tau], device=q.device, dtype=torch.float32)
+    rc = lib.pnfx_flash_fwd(*p4(q), *p4(k), *p4(v), *p4(o), o_lo.data_ptr(), M.data_ptr(),
+                            Z.data_ptr(), Nm.data_ptr(), mask.data_ptr(),
+                            ws.data_ptr() if with_workspace else None, nws if with_workspace else 0,
+                            B, H, N, D, t32.data_ptr(), scale, 0.5, 1, 1, _lib.PNFX_BF16,
+                            torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.pnfx_last_error()
+    torch.cuda.synchronize()
+    return o, o_lo, M, Z, Nm, mask
+
+
+@pytest.mark.parametrize("D", [16, 64])
+@pytest.mark.parametrize("tau", [0.0, 0.25, 1.0])
+def test_flash_silent_tile_bound_changes_nothing(dev, D, tau):
+    """The forward with the Cauchy-Schwarz tile bound (workspace given) is bitwise the
+    forward without it.  Inputs: zeroed key blocks and query blocks scaled down so that
+    whole tiles -- for single waves and for whole workgroups -- fall under the bound."""
+    print(f"[flash bound D={D} tau={tau}]", flush=True)
+    B, H, N = 2, 2, 1000
+    q = seeded((B, H, N, D), 60, torch.bfloat16, dev)
+    k = seeded((B, H, N, D), 61, torch.bfloat16, dev)
+    v = seeded((B, H, N, D), 62, torch.bfloat16, dev)
+    k[:, :, 128:256] = 0
+    k[0, 1, 640:704] = 0
+    q[:, :, 256:512] *= 0.05   # two 128-row query blocks: every wave bounded at tau >= 0.25
+    q[1, 0, 800:832] *= 0.02   # a single wave
+    scale = 1.0 / np.sqrt(D)
+    a = _fwd_abi(q, k, v, tau, scale, True)
+    b = _fwd_abi(q, k, v, tau, scale, False)
+    for name, x, y in zip(("O", "O_lo", "M", "Z", "Nmax", "mask"), a, b):
+        assert torch.equal(x, y), name
+    if tau > 0:  # the bound did apply somewhere: those tiles are silent in the mask
+        assert int(b[5].sum()) < b[5].numel()
+
+
+@pytest.mark.parametrize("rel", [-1e-3, 1e-3, 1e-2])
+def test_flash_silent_tile_bound_equality_case(dev, rel):
+    """Cauchy-Schwarz holds with equality for parallel q and k: every score equals
+    |q| |k| scale - tau.  tau = (1 + rel) |q| |k| scale: 0.1 % below keeps every causal tile
+    active (the bound, with its 2^-8 margin, must not fire); 0.1 % above makes the tiles
+    silent by their scores (inside the margin); 1 % above makes them silent by the bound.
+    Outputs, tie counts and mask match the oracle in every case."""
+    B, H, N, D = 1, 1, 256, 64
+    c = 0.75
+    q = torch.full((B, H, N, D), c, device=dev, dtype=torch.bfloat16)
+    k = torch.full((B, H, N, D), c, device=dev, dtype=torch.bfloat16)
+    v = seeded((B, H, N, D), 63, torch.bfloat16, dev)
+    scale = 0.125
+    tau = c * c * D * scale * (1 + rel)
+    o, o_lo, M, Z, Nm, mask = _fwd_abi(q, k, v, tau, scale, True)
+    Of, Mo, Zo, No = O.flash_fwd(to_np64(q), to_np64(k), to_np64(v), tau, scale, 0.5, True)
+    assert_bf16_close(to_np64(o), Of, "O")
+    m64 = tile_mask_64(mask).cpu().numpy().reshape(4, 4).astype(bool)
+    causal = np.tril(np.ones((4, 4), dtype=bool))
+    assert np.array_equal(m64, causal if rel < 0 else np.zeros((4, 4), dtype=bool))
+    assert np.array_equal(Nm.cpu().numpy().reshape(-1), No.reshape(-1))
+
+
 def test_flash_backward_is_deterministic(dev):
     B, H, N, D = 2, 2, 512, 64
     q = seeded((B, H, N, D), 50, torch.bfloat16, dev)

@@ -128,8 +128,8 @@ def test_c_abi_library_exports_every_declared_symbol():
 
 def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     lib = _lib.lib()
-    rc = lib.pnfx_flash_fwd(*([None, 0, 0, 0] * 4), None, None, None, None, None, 1, 1, 8, 48, None,
-                            0.125, 0.5, 1, 1, 1, None)
+    rc = lib.pnfx_flash_fwd(*([None, 0, 0, 0] * 4), None, None, None, None, None, None, 0,
+                            1, 1, 8, 48, None, 0.125, 0.5, 1, 1, 1, None)
     assert rc == -1 and b"head dim" in lib.pnfx_last_error()
     rc = lib.pnfx_fir_fwd(None, 0, 0, 0, None, 1, 1, 4, 8, None, 1, 7, 1, None)
     assert rc == -1 and b"null" in lib.pnfx_last_error()
