@@ -336,6 +336,54 @@ __global__ __launch_bounds__(256) void flash_key_norm_kernel(FwdParams p) {
   if (lane == 0) p.knorm[tile] = sqrtf(ss);
 }
 
+// Without tie counting the forward needs no rectified copy of the scores.  Each query row's
+// maximum of u = relu(s) is max(0, max s): an integer max from 0 over the raw bit patterns
+// (positive floats order as their bits; negative ones are negative integers).  P = u^10 is
+// formed from the raw score: t = s |s| carries the sign of s into the chain t^2, t^4,
+// t^4 t = sign(s) s^10 -- for s > 0 the very multiplies of u^2, u^4, u^8, u^8 u^2 -- and a
+// signed 16-bit max with 0 on the packed bf16 values turns the negative ones (s < 0, and the
+// masked -1) into +0: half a VALU op per score instead of a rectifier on every score.
+// Bit patterns through by-value helpers: clang's __builtin_bit_cast applied directly to an
+// ext_vector element (v[i]) reads element 0 whatever i is.
+__device__ __forceinline__ int f2i(float x) { return __builtin_bit_cast(int, x); }
+__device__ __forceinline__ float i2f(int x) { return __builtin_bit_cast(float, x); }
+
+__device__ __forceinline__ void row_max_kq(const f32x4 (&s)[2][2], float (&tm)[2]) {
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    int mx = 0;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = max(mx, f2i(s[kk][qb][i]));
+    tm[qb] = i2f(mx);
+  }
+}
+__device__ __forceinline__ float pow10_signed(float s) {
+  const float t = s * __builtin_fabsf(s);
+  const float t2 = t * t;
+  const float t4 = t2 * t2;
+  return t4 * t;
+}
+// Two floats to a packed bf16 pair (RNE), negative results to +0.
+__device__ __forceinline__ uint32_t pack2_relu(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 v = __builtin_convertvector((f32x2){a, b}, bf16x2);
+  const s16x2 z = {0, 0};
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(s16x2, v), z));
+}
+__device__ __forceinline__ bf16x8 pack8_relu(float a0, float a1, float a2, float a3, float b0,
+                                             float b1, float b2, float b3) {
+  const u32x4 w = {pack2_relu(a0, a1), pack2_relu(a2, a3), pack2_relu(b0, b1), pack2_relu(b2, b3)};
+  return __builtin_bit_cast(bf16x8, w);
+}
+// max of two non-negative floats as an integer max (no canonicalising operand copies)
+__device__ __forceinline__ float max_nonneg(float a, float b) {
+  return __builtin_bit_cast(float, max(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b)));
+}
+
 // COUNT: also count the peak ties (Nmax); the training path leaves that to the backward.
 template <int D, bool CAUSAL, bool PS, bool COUNT>
 __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdParams p) {
@@ -439,8 +487,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
     qb_w = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, qb_w)));
     qb_wg = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, qb_wg)));
   }
-  float kn_cur = bound ? kn[0] : 0.f;                   // tile t
-  float kn_next = (bound && ntiles > 1) ? kn[1] : 0.f;  // tile t + 1
+  // wave-uniform: kept in scalar registers
+  float kn_cur = bound ? i2f(__builtin_amdgcn_readfirstlane(f2i(kn[0]))) : 0.f;  // tile t
+  float kn_next = (bound && ntiles > 1) ? i2f(__builtin_amdgcn_readfirstlane(f2i(kn[1]))) : 0.f;
 
   // Software pipeline: tile t+1 streams from HBM/L2 straight into one LDS buffer while tile
   // t is computed from the other; one barrier per tile.
@@ -458,7 +507,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
     const bool bounded = bound && qb_w * kn_cur <= tau;  // implied for every unloaded tile
     kn_cur = kn_next;
     if (bound && t + 2 < ntiles)
-      kn_next = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, kn[t + 2])));
+      kn_next = i2f(__builtin_amdgcn_readfirstlane(f2i(kn[t + 2])));
     bool active = false;
     if (has_rows && !bounded && !(CAUSAL && n0 > qrow0 + 31)) {
       const bf16* Kc = bc.k;
@@ -485,13 +534,14 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
         float tm[2];
         affine_kq<PS>(s, scale, ntau);
         if (masked) mask_kq(s, n0, hf, qrow0, N, CAUSAL, g, r16);
-        rectify_kq(s, tm);
-        if (!__any(fmaxf(tm[0], tm[1]) > 0.f)) continue;  // silent half: skip P and P.V
+        if constexpr (COUNT) rectify_kq(s, tm);
+        else row_max_kq(s, tm);
+        if (!__any(max_nonneg(tm[0], tm[1]) > 0.f)) continue;  // silent half: skip P and P.V
         active = true;
         bf16x8 pf[2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
-          const float mnew = fmaxf(mrun[qb], tm[qb]);
+          const float mnew = max_nonneg(mrun[qb], tm[qb]);
           if (COUNT) {
             int c = (mnew == mrun[qb]) ? cnt[qb] : 0;
 #pragma unroll
@@ -501,9 +551,15 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
             cnt[qb] = c;
           }
           mrun[qb] = mnew;
-          pf[qb] = pack8(pow10f_(s[0][qb][0]), pow10f_(s[0][qb][1]), pow10f_(s[0][qb][2]),
-                         pow10f_(s[0][qb][3]), pow10f_(s[1][qb][0]), pow10f_(s[1][qb][1]),
-                         pow10f_(s[1][qb][2]), pow10f_(s[1][qb][3]));
+          if constexpr (COUNT)
+            pf[qb] = pack8(pow10f_(s[0][qb][0]), pow10f_(s[0][qb][1]), pow10f_(s[0][qb][2]),
+                           pow10f_(s[0][qb][3]), pow10f_(s[1][qb][0]), pow10f_(s[1][qb][1]),
+                           pow10f_(s[1][qb][2]), pow10f_(s[1][qb][3]));
+          else
+            pf[qb] = pack8_relu(
+                pow10_signed(s[0][qb][0]), pow10_signed(s[0][qb][1]), pow10_signed(s[0][qb][2]),
+                pow10_signed(s[0][qb][3]), pow10_signed(s[1][qb][0]), pow10_signed(s[1][qb][1]),
+                pow10_signed(s[1][qb][2]), pow10_signed(s[1][qb][3]));
         }
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
