@@ -306,7 +306,9 @@ def zipf_tokens(batch, seq, vocab, seed, s=1.1):
 
 def bench_lm(dev, steps=10, warmup=3):
     """C3: one training step of the 6-layer LM with flash pn_fir_tau attention (bf16 autocast,
-    AdamW), eager and captured as one HIP graph.  Synthetic Zipf tokens, random init, dropout 0."""
+    AdamW), eager and captured as one HIP graph.  Synthetic Zipf tokens, random init, dropout 0.
+    Eager with the reference's AdamW (foreach) and with torch's fused AdamW; the graph with the
+    fused, capturable AdamW (so eager_fused and graph do the same work)."""
     from paper_01_anti_decoy_pnfirtau_amd.wikilm import (GraphedStep, WikiLM, WikiLMConfig,
                                                           make_optimizer, train_step)
 
@@ -321,7 +323,12 @@ def bench_lm(dev, steps=10, warmup=3):
     out["eager_ms_per_step"] = round(wall, 3)
     torch.manual_seed(0)
     model = WikiLM(C3["vocab"], cfg, "pn_fir_tau_flash").to(dev)
-    opt = make_optimizer(model, cfg, capturable=True)
+    opt = make_optimizer(model, cfg, fused=True)
+    wall_f, _ = time_steps(lambda: train_step(model, opt, x), steps, warmup)
+    out["eager_fused_adamw_ms_per_step"] = round(wall_f, 3)
+    torch.manual_seed(0)
+    model = WikiLM(C3["vocab"], cfg, "pn_fir_tau_flash").to(dev)
+    opt = make_optimizer(model, cfg, capturable=True, fused=True)
     g = GraphedStep(model, opt, x.clone())
     wall_g, _ = time_steps(g.replay, steps, warmup)
     out["graph_ms_per_step"] = round(wall_g, 3)

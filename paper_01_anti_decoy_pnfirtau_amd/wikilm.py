@@ -105,10 +105,15 @@ class WikiLM(nn.Module):
         return self.head(self.ln_f(h))
 
 
-def make_optimizer(model: nn.Module, cfg: WikiLMConfig, capturable: bool = False):
-    """AdamW as the reference builds it (experiments/exp4_wikitext2_lm.py:326-328)."""
+def make_optimizer(model: nn.Module, cfg: WikiLMConfig, capturable: bool = False,
+                   fused: bool | None = None):
+    """AdamW as the reference builds it (experiments/exp4_wikitext2_lm.py:326-328).
+
+    ``fused=True`` selects torch's single-kernel AdamW (same update rule); with
+    ``capturable=True`` it is the cheapest optimizer step to capture in a graph.
+    """
     return torch.optim.AdamW(model.parameters(), lr=cfg.lr, betas=(0.9, 0.95),
-                             weight_decay=cfg.weight_decay, capturable=capturable)
+                             weight_decay=cfg.weight_decay, capturable=capturable, fused=fused)
 
 
 def lm_loss(model: nn.Module, x: torch.Tensor, amp: bool) -> torch.Tensor:
