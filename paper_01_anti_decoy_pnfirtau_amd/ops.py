@@ -12,6 +12,8 @@ pnfx::flash_fwd/_bwd   _FlashPnFirTauFn                 :814-968
 """
 from __future__ import annotations
 
+import functools
+
 import torch
 from torch import Tensor
 
@@ -194,6 +196,11 @@ def _new_o(q: Tensor, o_bnhd: bool) -> Tensor:
     return torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
 
 
+@functools.lru_cache(maxsize=None)
+def _fwd_workspace_bytes(B: int, H: int, N: int, D: int) -> int:
+    return int(_lib.lib().pnfx_flash_fwd_workspace_size(B, H, N, D))
+
+
 @torch.library.custom_op("pnfx::flash_fwd", mutates_args=(), device_types="cuda")
 def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma: float,
               has_gamma: bool, causal: bool, o_bnhd: bool,
@@ -216,11 +223,15 @@ def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma:
     M = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     Z = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     Nm = torch.empty((B, H, N) if with_nmax else (0,), device=q.device, dtype=torch.int32)
-    mask = torch.empty((B * H, (N + 31) // 32, (N + 63) // 64), device=q.device, dtype=torch.uint8)
+    # one allocation: the tile mask, then (256-byte aligned) the workspace of the silent-tile
+    # bound (per-tile key norms, a few KiB)
+    mshape = (B * H, (N + 31) // 32, (N + 63) // 64)
+    mbytes = (mshape[0] * mshape[1] * mshape[2] + 255) // 256 * 256
+    nws = _fwd_workspace_bytes(B, H, N, D)
+    buf = torch.empty(mbytes + nws, device=q.device, dtype=torch.uint8)
+    mask = buf[:mshape[0] * mshape[1] * mshape[2]].view(mshape)
+    ws = buf[mbytes:]
     t32 = _tau32(tau)
-    # workspace of the silent-tile bound (per-tile key norms; a few KiB)
-    nws = _lib.lib().pnfx_flash_fwd_workspace_size(B, H, N, D)
-    ws = torch.empty(nws, device=q.device, dtype=torch.uint8)
     rc = _lib.lib().pnfx_flash_fwd(
         *_ptr4(q), *_ptr4(k), *_ptr4(v), *_ptr4(o), o_lo.data_ptr() if bf else None,
         M.data_ptr(), Z.data_ptr(), Nm.data_ptr() if with_nmax else None, mask.data_ptr(),
