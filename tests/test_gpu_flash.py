@@ -173,6 +173,7 @@ SILENT_KEY_CASES = [
     (640, 128, True, "even"),
     (512, 64, False, "odd"),
     (384, 16, True, "all_but_last"),
+    (300, 32, True, "odd"),
     (256, 64, True, "all"),
 ]
 
@@ -273,6 +274,62 @@ def test_flash_silent_tile_bound_equality_case(dev, rel):
     causal = np.tril(np.ones((4, 4), dtype=bool))
     assert np.array_equal(m64, causal if rel < 0 else np.zeros((4, 4), dtype=bool))
     assert np.array_equal(Nm.cpu().numpy().reshape(-1), No.reshape(-1))
+
+
+def test_flash_backward_stages_called_separately_match_one_call(dev):
+    """pnfx_flash_bwd_stages run as three calls (prepare, dQ, dK/dV) on one workspace gives
+    bitwise the outputs of one pnfx_flash_bwd call -- with planted silent key tiles, so the
+    dK/dV stage's tile order depends on the activity the dQ stage recorded."""
+    from paper_01_anti_decoy_pnfirtau_amd import _lib, ops
+    lib = _lib.lib()
+    B, H, N, D = 1, 2, 700, 64
+    q = seeded((B, H, N, D), 70, torch.bfloat16, dev)
+    k = seeded((B, H, N, D), 71, torch.bfloat16, dev)
+    v = seeded((B, H, N, D), 72, torch.bfloat16, dev)
+    dO = seeded((B, H, N, D), 73, torch.bfloat16, dev)
+    for j in (0, 2, 3, 6, 9):
+        k[:, :, 64 * j:64 * j + 64] = 0
+    tau = torch.tensor(0.25, device=dev)
+    scale = 1.0 / np.sqrt(D)
+    o, o_lo, M, Z, _, mask = torch.ops.pnfx.flash_fwd(q, k, v, tau, scale, 0.5, True, True,
+                                                      False, False)
+    nws = lib.pnfx_flash_bwd_workspace_size(B, H, N, D)
+
+    def run(stage_list):
+        ws = torch.empty(nws, device=dev, dtype=torch.uint8)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        dt = torch.zeros((), device=dev)
+        for st in stage_list:
+            rc = lib.pnfx_flash_bwd_stages(
+                st, *ops._ptr4(q), *ops._ptr4(k), *ops._ptr4(v), *ops._ptr4(o), o_lo.data_ptr(),
+                *ops._ptr4(dO), M.data_ptr(), Z.data_ptr(), mask.data_ptr(), *ops._ptr4(dq),
+                *ops._ptr4(dk), *ops._ptr4(dv), dt.data_ptr(), ws.data_ptr(), nws, B, H, N, D,
+                tau.data_ptr(), scale, 0.5, 1, 1, _lib.PNFX_BF16,
+                torch.cuda.current_stream().cuda_stream)
+            assert rc == 0, lib.pnfx_last_error()
+        torch.cuda.synchronize()
+        return dq, dk, dv, dt
+
+    one = run([_lib.PNFX_BWD_ALL])
+    three = run([_lib.PNFX_BWD_PREPARE, _lib.PNFX_BWD_DQ, _lib.PNFX_BWD_DKDV])
+    for name, a, b in zip(("dq", "dk", "dv", "dtau"), one, three):
+        assert torch.equal(a, b), name
+    assert torch.all(one[1][:, :, 0:64] == 0)  # a silent key block
+
+
+def test_flash_silent_tile_bound_off_past_its_tile_limit(dev):
+    """Past 1024 key tiles (N > 65536) the forward runs without the bound; with the workspace
+    given it is still bitwise the forward without it."""
+    print("[flash bound past tile limit]", flush=True)
+    B, H, N, D = 1, 1, 65600, 16
+    q = seeded((B, H, N, D), 64, torch.bfloat16, dev)
+    k = seeded((B, H, N, D), 65, torch.bfloat16, dev)
+    v = seeded((B, H, N, D), 66, torch.bfloat16, dev)
+    k[:, :, :4096] = 0
+    a = _fwd_abi(q, k, v, 0.5, 0.25, True)
+    b = _fwd_abi(q, k, v, 0.5, 0.25, False)
+    for name, x, y in zip(("O", "O_lo", "M", "Z", "Nmax", "mask"), a, b):
+        assert torch.equal(x, y), name
 
 
 def test_flash_backward_is_deterministic(dev):
