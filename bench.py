@@ -468,7 +468,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
+        print("bench.py measures one GPU: this build has no multi-GPU path (the operator "
+              "shards over independent (b, h) slices; only dtau joins the gradient all-reduce)",
               file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
