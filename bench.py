@@ -20,7 +20,11 @@ Also measured in the same run and reported on the same JSON line:
 * ``cpu_baseline``: the numpy oracle (float32) forward + backward on one (b, h)
   slice of C4 on this host's cores.
 
-``--only flash|fir|copy`` runs a single short workload (for rocprofv3 passes).
+``--only MODE`` runs one workload alone and prints its own JSON (for rocprofv3 passes and
+per-stage timing): flash (C4 step), flash_c5 (C5 step), fir, copy (512 MiB device copy, the
+counter calibration), rows (row-fused score kernels on the C3 scores), lm (C3 LM step),
+mha6 (the 6-layer stack), ref (the reference's published shapes), kernels (per-stage HIP
+events at C4, C4 50 % silent and C5).
 """
 from __future__ import annotations
 
@@ -462,8 +466,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["flash", "fir", "copy", "lm", "mha6", "ref", "kernels",
-                                       "rows"],
+    ap.add_argument("--only", choices=["flash", "flash_c5", "fir", "copy", "lm", "mha6", "ref",
+                                       "kernels", "rows"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -492,6 +496,14 @@ def main():
         return
     if args.only == "rows":
         print(json.dumps(bench_rows(dev)))
+        return
+    if args.only == "flash_c5":  # the C5 step alone (for a kernel trace of its own)
+        q5, k5, v5, dO5 = make_inputs(C5["B"], C5["H"], C5["N"], C5["D"], 1, dev,
+                                      std=C5["D"] ** -0.25)
+        wall5, ev5 = time_steps(flash_step_fn(q5, k5, v5, dO5, 0.0), args.steps, args.warmup)
+        flops5 = 7 * gemm_flops(C5["B"], C5["H"], C5["N"], C5["D"])
+        print(json.dumps({"ms_per_step": wall5, "event_ms": ev5,
+                          "tflops": flops5 / (wall5 * 1e-3) / 1e12}))
         return
     if args.only == "kernels":  # per-stage HIP-event times at C4 and C5
         out = {}
