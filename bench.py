@@ -17,8 +17,9 @@ Also measured in the same run and reported on the same JSON line:
   taps) in GB/s, rotating 20 input/output buffer pairs (640 MiB) so the 256 MB
   Infinity Cache cannot serve repeats;
 * ``wide_head``: config C5 (B=8, H=8, N=4096, d=128) TFLOP/s;
-* ``cpu_baseline``: the numpy oracle (float32) forward + backward on one (b, h)
-  slice of C4 on this host's cores.
+* ``cpu_baseline``: the reference's CPU path on this host's cores -- the eager
+  PnFirTauMHA fp32 forward + backward at config C1 (the headline CPU figure), the eager
+  causal_fir at C2, and the numpy flash restatement on C4 slices extrapolated to a step.
 
 ``--only MODE`` runs one workload alone and prints its own JSON (for rocprofv3 passes and
 per-stage timing): flash (C4 step), flash_c5 (C5 step), fir, copy (512 MiB device copy, the
@@ -294,27 +295,13 @@ def profiled_traffic(kernel):
 C3 = dict(n_layers=6, d_model=256, n_heads=4, d_ff=1024, seq=512, batch=32, vocab=33278)
 
 
-def zipf_tokens(batch, seq, vocab, seed, s=1.1):
-    """Token ids ~ Zipf(s) truncated to [0, vocab) (rejection), seeded on the CPU."""
-    import numpy as np
-
-    rng = np.random.default_rng(seed)
-    need, out = batch * seq, []
-    while need > 0:
-        z = rng.zipf(s, size=2 * need) - 1
-        z = z[z < vocab][:need]
-        out.append(z)
-        need -= len(z)
-    return torch.from_numpy(np.concatenate(out).reshape(batch, seq).astype(np.int64))
-
-
 def bench_lm(dev, steps=10, warmup=3):
     """C3: one training step of the 6-layer LM with flash pn_fir_tau attention (bf16 autocast,
     AdamW), eager and captured as one HIP graph.  Synthetic Zipf tokens, random init, dropout 0.
     Eager with the reference's AdamW (foreach) and with torch's fused AdamW; the graph with the
     fused, capturable AdamW (so eager_fused and graph do the same work)."""
     from paper_01_anti_decoy_pnfirtau_amd.wikilm import (GraphedStep, WikiLM, WikiLMConfig,
-                                                          make_optimizer, train_step)
+                                                          make_optimizer, train_step, zipf_tokens)
 
     cfg = WikiLMConfig(d_model=C3["d_model"], n_heads=C3["n_heads"], n_layers=C3["n_layers"],
                        d_ff=C3["d_ff"], max_seq=C3["seq"], dropout=0.0)
@@ -438,27 +425,98 @@ def bench_reference_configs(dev, steps=30, warmup=10):
     return out
 
 
-def cpu_baseline(slices=8):
-    """numpy oracle (float32) forward + backward on `slices` (b, h) slices of C4."""
+def _cpu_info():
+    """CPU model, logical cores this process may run on, and the threads torch will use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    # the box's CPU share is set by OMP_NUM_THREADS; never more threads than cores we may use
+    threads = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    return model, cores, threads
+
+
+def _median_ms(fn, warmup, reps):
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2], ts[len(ts) // 4], ts[(3 * len(ts)) // 4]
+
+
+def cpu_baseline(warmup=10, reps=50):
+    """The reference's CPU path, timed on this host: the eager PnFirTauMHA (the package's
+    restatement of src/pnfirtau_attention.py:195-247, pure PyTorch) fp32 forward + backward at
+    C1 (B=2, N=128, D=64, H=4), median of `reps` after `warmup`; the eager causal_fir at C2
+    ([B*H=64, N=2048, C=64] bf16, the reference's CPU FIR, src/pnfirtau_attention.py:65-74);
+    and, as a secondary figure, the numpy float32 flash restatement on two (b, h) slices of C4,
+    extrapolated x B*H to one C4 step."""
     import numpy as np
+
+    from paper_01_anti_decoy_pnfirtau_amd import PnFirConfig, PnFirTauMHA, causal_fir
+
+    model, cores, threads = _cpu_info()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        B, N, Dm, H = 2, 128, 64, 4
+        torch.manual_seed(0)
+        m = PnFirTauMHA(PnFirConfig(d_model=Dm, n_heads=H, dropout=0.0))
+        g = torch.Generator().manual_seed(1)
+        x = torch.randn(B, N, Dm, generator=g).requires_grad_(True)
+        dy = torch.randn(B, N, Dm, generator=g)
+
+        def c1():
+            m.zero_grad(set_to_none=True)
+            x.grad = None
+            m(x).backward(dy)
+
+        med, q1, q3 = _median_ms(c1, warmup, reps)
+        hd = Dm // H
+        c1_flop = 7 * B * H * N * N * hd  # the attention's algorithmic FLOP, as the GPU metric
+        gx = torch.Generator().manual_seed(2)
+        xf = torch.randn(64, 2048, 64, generator=gx).to(torch.bfloat16)
+        taps = torch.rand(7, generator=gx)
+        taps = taps / taps.sum()
+        fmed, _, _ = _median_ms(lambda: causal_fir(xf, taps), 3, 20)
+        fir_bytes = 2 * 64 * 2048 * 64 * 2
+    finally:
+        torch.set_num_threads(prev)
 
     from oracle import pnfirtau_oracle as O
 
-    N, D = C4["N"], C4["D"]
+    Nc, Dc, slices = C4["N"], C4["D"], 2
     rng = np.random.default_rng(0)
     dt = 0.0
     for _ in range(slices):
-        q, k, v, dO = (rng.standard_normal((1, 1, N, D)).astype(np.float32) for _ in range(4))
+        q, k, v, dO = (rng.standard_normal((1, 1, Nc, Dc)).astype(np.float32) for _ in range(4))
         t0 = time.perf_counter()
         O.flash_fwd(q, k, v, 0.0, dtype=np.float32)
         O.flash_bwd(q, k, v, 0.0, dO, dtype=np.float32)
         dt += time.perf_counter() - t0
-    flops = 7 * N * N * D * slices
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{slices} (b,h) slices of C4 (N={N}, d={D}) fwd+bwd, numpy float32 oracle, "
-                      f"{dt:.2f} s; BLAS on {threads} threads, elementwise on 1"}
+    c4_step_s = dt / slices * C4["B"] * C4["H"]
+    return {"value": round(c1_flop / (med * 1e-3) / 1e12, 6), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"C1 eager PnFirTauMHA fp32 fwd+bwd (B=2, N=128, D=64, H=4), median of "
+                      f"{reps} after {warmup} warm-up: {med:.3f} ms (IQR {q1:.3f}-{q3:.3f}); "
+                      f"TFLOP/s of the attention's 7*B*H*N^2*d FLOP",
+            "cpu_model": model, "logical_cores_available": cores, "torch_threads": threads,
+            "c1_ms_per_fwd_bwd": round(med, 4),
+            "fir_c2": {"what": "eager causal_fir (conv1d) on [64, 2048, 64] bf16, shared 7 taps",
+                       "ms": round(fmed, 3), "gbps": round(fir_bytes / (fmed * 1e-3) / 1e9, 2)},
+            "c4_extrapolated": {"what": f"numpy float32 flash restatement, {slices} (b,h) slices of "
+                                        f"C4 fwd+bwd, x B*H", "s_per_step": round(c4_step_s, 2),
+                                "tflops": round(7 * gemm_flops(**C4) / c4_step_s / 1e12, 6)}}
 
 
 def main():

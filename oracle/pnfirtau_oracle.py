@@ -16,6 +16,7 @@ reference repository root):
 * ``power_norm_peak_gate`` (+bwd) src/pnfirtau_attention.py:87-119
 * ``pn_rows_fwd`` / ``pn_rows_bwd`` src/triton_pnfirtau.py:141-303, 694-811
 * ``flash_fwd`` / ``flash_bwd``   src/triton_pnfirtau.py:313-621, 814-983
+* ``flash_reference_bf16``       the same, with the reference kernels' bf16 rounding points
 * ``mha_fwd_bwd``               src/pnfirtau_attention.py:195-247 (PnFirTauMHA)
 * ``tile_activity``             experiments/exp4b_mha6_instrumentation.py:80-128
 
@@ -358,12 +359,18 @@ def _flash_scores(q, k, tau, scale, causal, dtype):
     return s, valid
 
 
-def flash_fwd(q, k, v, tau, scale=None, gamma=0.5, causal=True, dtype=np.float64):
+def flash_fwd(q, k, v, tau, scale=None, gamma=0.5, causal=True, dtype=np.float64,
+              p_bf16=False):
     """Flash forward semantics on [..., N, d]: returns (O, M, Z, Nmax).
 
     u = relu(q k^T * scale - tau) on valid entries; P = u^10; Z = sum P + 1e-12;
     M = max u; Nmax = #(u == M) when M > 0 else 0; gate = M/(M+gamma) (0 when
     M <= 0); O = (P v) * gate / Z  (src/triton_pnfirtau.py:383-443).
+
+    ``p_bf16``: P rounded to bf16 before it weights v and enters Z -- the weights a bf16
+    kernel multiplies v by (src/triton_pnfirtau.py:417-420); the reference's kernel sums the
+    unrounded P into its mass (:405), the default here.  Each rounded term is within
+    the bf16 unit roundoff 2^-8 of P.
     """
     q = np.asarray(q)
     if scale is None:
@@ -371,6 +378,8 @@ def flash_fwd(q, k, v, tau, scale=None, gamma=0.5, causal=True, dtype=np.float64
     s, valid = _flash_scores(q, np.asarray(k), tau, scale, causal, dtype)
     u = np.where(valid & (s > 0), s, 0).astype(dtype)
     P = _pow_p(u, 10.0)
+    if p_bf16:
+        P = round_bf16(P).astype(dtype)
     mass = P.sum(axis=-1)
     Z = mass + dtype(EPS_Z)
     M = u.max(axis=-1)
@@ -423,6 +432,45 @@ def flash_bwd(q, k, v, tau, dO, scale=None, gamma=0.5, causal=True, return_abs=F
     if return_abs:  # sum |du|: the conditioning scale of the dtau sum
         return dq, dk, dv, -du.sum(), np.abs(du).sum()
     return dq, dk, dv, -du.sum()
+
+
+def flash_reference_bf16(q, k, v, tau, dO, scale=None, gamma=0.5, causal=True):
+    """The reference kernels' bf16 rounding points, float64 everywhere else: returns
+    (O, dq, dk, dv, dtau) as the reference's bf16 forward and backward would form them.
+
+    Forward (src/triton_pnfirtau.py:405, :417-420, :422-429): P = u^10 weights v after
+    rounding to bf16, the mass sums the unrounded P, and O is stored in bf16.  Backward
+    (:566-571, :575-577, :590-600): w = u^10 g/Z is rounded to bf16 for dV; D = <dO, O>/g
+    uses the stored bf16 O; dS = du * scale is rounded to bf16 for dK and dQ; dtau = -sum du
+    is not rounded.  Inputs are taken as given (already bf16-valued).  This is the error a
+    bf16 kernel with the reference's structure carries, for comparison with the HIP kernels'.
+    """
+    q, k, v, dO = (np.asarray(t, dtype=np.float64) for t in (q, k, v, dO))
+    if scale is None:
+        scale = 1.0 / np.sqrt(q.shape[-1])
+    s, valid = _flash_scores(q, k, tau, scale, causal, np.float64)
+    u = np.where(valid & (s > 0), s, 0.0)
+    P = _pow_p(u, 10.0)
+    Z = (P.sum(axis=-1) + EPS_Z)[..., None]
+    M = u.max(axis=-1)[..., None]
+    nmax = (u == M).sum(axis=-1, keepdims=True)
+    has_gamma = gamma is not None and gamma > 0
+    g = np.where(M > 0, M / (M + gamma), 0.0) if has_gamma else np.where(M > 0, 1.0, 0.0)
+    rb = lambda a: round_bf16(a).astype(np.float64)  # noqa: E731
+    O = rb(np.matmul(rb(P), v) * (g / Z))
+    w = P * g / Z
+    dv = np.matmul(np.swapaxes(rb(w), -1, -2), dO)
+    dW = np.matmul(dO, np.swapaxes(v, -1, -2))
+    D = np.where(g > 0, (dO * O).sum(axis=-1, keepdims=True) / np.where(g > 0, g, 1.0), 0.0)
+    du = (10.0 * g / Z) * u**9 * (dW - D)
+    if has_gamma:
+        tie = (u == M) & (M > 0)
+        du = du + np.where(tie, D * gamma / (M + gamma) ** 2 / np.maximum(nmax, 1), 0.0)
+    du = np.where(u > 0, du, 0.0)
+    dS = rb(du * scale)
+    dq = np.matmul(dS, k)
+    dk = np.matmul(np.swapaxes(dS, -1, -2), q)
+    return O, dq, dk, dv, -du.sum()
 
 
 def tile_activity(q, k, tau, scale=None, causal=True, tile=64):

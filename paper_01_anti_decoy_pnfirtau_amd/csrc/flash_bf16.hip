@@ -296,8 +296,8 @@ __device__ __forceinline__ void rectify_kq(f32x4 (&s)[2][2], float (&tm)[2]) {
   }
 }
 
-// Silent-tile bound.  Every score of a (query, key) pair is at most |q| |k| scale - tau
-// (Cauchy-Schwarz), so a tile whose largest query norm times largest key norm times scale
+// Silent-tile bound.  Every score of a (query, key) pair is at most |q| |k| |scale| - tau
+// (Cauchy-Schwarz), so a tile whose largest query norm times largest key norm times |scale|
 // is <= tau has no positive rectified score.  The MFMA's own rounding and that of the norms
 // are far below the 2^-8 margin, so the test never drops an active tile.  The key side is
 // one norm per 64-key tile, from this pass; the query side is formed by each forward wave.
@@ -479,10 +479,12 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
   if (bound) {
     for (int i = tid; i < ntiles; i += 256) kn_s[i] = p.knorm[(int64_t)bh * p.nk64 + i];
     qss = wave_max(qss);
-    qb_w = sqrtf(qss) * scale * kBoundMargin;
+    // |scale|: with a negative scale the bound is |q| |k| |scale| - tau just the same
+    qb_w = sqrtf(qss) * fabsf(scale) * kBoundMargin;
     if (lane == 0) qss_s[w] = qss;
     __syncthreads();
-    qb_wg = sqrtf(fmaxf(fmaxf(qss_s[0], qss_s[1]), fmaxf(qss_s[2], qss_s[3]))) * scale * kBoundMargin;
+    qb_wg = sqrtf(fmaxf(fmaxf(qss_s[0], qss_s[1]), fmaxf(qss_s[2], qss_s[3]))) * fabsf(scale) *
+            kBoundMargin;
     // wave-uniform: keep them in scalar registers
     qb_w = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, qb_w)));
     qb_wg = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, qb_wg)));
@@ -632,8 +634,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
 //   dS_ij = 10 scale x_i [u_ij^9 (dW_ij - D_i) + [u_ij == M_i] G''_i/Nmax_i],
 //   G''_i = D_i gate'(M_i) / (10 x_i),
 // which is how the dQ kernel forms it: the dW MFMA accumulator starts at -D_i, the bracket
-// costs one FMA per score after the power chain, and the row factor 10 scale x_i is applied
-// to dQ and to the tau partials once, at the end.  The dK/dV kernel needs the row factor
+// costs one FMA per score after the power chain, and the row factor is applied once, at
+// the end: 10 scale x_i to dQ, 10 x_i to the tau partials (sums of du = dS/scale, so that
+// dtau = -sum du needs no division by scale).  The dK/dV kernel needs the row factor
 // inside its sums over rows; there, with rho_i = x_i^(1/10), a = rho u and
 // kappa_i = 10 scale rho_i, the dV weight is w = u^10 x = a^10 and
 //   dS_ij = a^9 (kappa_i dW_ij - kappa_i D_i) + [u_ij == M_i] G_i/Nmax_i,
@@ -912,7 +915,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
     multi = multi || (c > 1 && rG[qb] != 0.f);
     rG[qb] = c > 0 ? rG[qb] / (float)c : 0.f;  // for a second pass
   }
-  dsum = wave_sum_d(dsum) * (double)ds_mult;
+  // sum of du = dS / scale (no division by scale: scale may be 0)
+  dsum = wave_sum_d(dsum) * 10.0;
   if (lane == 0) p.partials[((int64_t)bh * nqb + qblk) * 4 + w] = dsum;
   // Second pass only if some row of the workgroup has several ties (also a barrier: the
   // last tile's LDS buffer is free before the first tile is staged again).
@@ -1291,10 +1295,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   }
 }
 
-// dtau = -(sum of all ds partials) / scale, summed in fp64 by one block in a fixed order
+// dtau = -(sum of all du partials), summed in fp64 by one block in a fixed order
 // (deterministic).  Each thread keeps four independent loads in flight.
 __global__ __launch_bounds__(1024) void flash_dtau_kernel(const double* partials, int64_t n,
-                                                          float scale, float* dtau) {
+                                                          float* dtau) {
   __shared__ double red[16];
   const int tid = threadIdx.x;
   double a[4] = {0.0, 0.0, 0.0, 0.0};
@@ -1309,7 +1313,7 @@ __global__ __launch_bounds__(1024) void flash_dtau_kernel(const double* partials
   __syncthreads();
   if (tid < 64) {
     acc = wave_sum_d(tid < 16 ? red[tid] : 0.0);
-    if (tid == 0) dtau[0] = (float)(-acc / (double)scale);
+    if (tid == 0) dtau[0] = (float)(-acc);
   }
 }
 
@@ -1373,7 +1377,7 @@ int launch_bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, h
     if (ps) launch_dq<D, true>(bp, causal, gdq, st);
     else launch_dq<D, false>(bp, causal, gdq, st);
     hipLaunchKernelGGL(flash_dtau_kernel, dim3(1), dim3(1024), 0, st, bp.partials,
-                       (int64_t)bp.B * bp.H * nqb * 4, bp.scale, bp.dtau);
+                       (int64_t)bp.B * bp.H * nqb * 4, bp.dtau);
     const int rc = launch_status("pnfx_flash_bwd(dq)");
     if (rc) return rc;
   }

@@ -113,17 +113,16 @@ __global__ __launch_bounds__(256) void f32_bwd_pre_kernel(BwdParams p) {
   const float M = p.M[row], Z = p.Z[row];
   const float g = M > 0.f ? (HAS_GAMMA ? M / (M + p.gamma) : 1.f) : 0.f;
   const float Dv = g > 0.f ? dot / g : 0.f;
-  float G = 0.f;  // the whole row's peak-tie gradient; the dQ kernel divides it by Nmax
-  if (HAS_GAMMA && M > 0.f) {
-    const float dgate = p.gamma / ((M + p.gamma) * (M + p.gamma));
-    G = Dv * dgate * p.scale;
-  }
+  float Gu = 0.f;  // the whole row's peak-tie du; the dQ kernel divides it by Nmax
+  if (HAS_GAMMA && M > 0.f) Gu = Dv * (p.gamma / ((M + p.gamma) * (M + p.gamma)));
   float* rc = p.rc + 8 * row;
   rc[0] = M;
   rc[1] = g / Z;
-  rc[2] = 10.f * g / Z * p.scale;
+  rc[2] = 10.f * g / Z * p.scale;  // dS = du scale, for the dK/dV kernel
   rc[3] = Dv;
-  rc[4] = G;
+  rc[4] = Gu * p.scale;  // the dQ kernel replaces it by its share G/Nmax
+  rc[5] = 10.f * g / Z;  // du, for the dQ kernel (its sum is the tau gradient)
+  rc[6] = Gu;
 }
 
 template <int D, bool CAUSAL>
@@ -146,7 +145,7 @@ __global__ __launch_bounds__(64) void f32_bwd_dq_kernel(BwdParams p) {
     dq[d] = 0.f;
   }
   float* rcp = p.rc + 8 * ((int64_t)bh * N + (has ? row : 0));
-  const float rM = rcp[0], rcoef = rcp[2], rD = rcp[3];
+  const float rM = rcp[0], rcoef = rcp[5], rD = rcp[3];
   const int kv_end = CAUSAL ? min((int)(blockIdx.x + 1) * TB, N) : N;
   const int ntiles = (kv_end + TB - 1) / TB;
   // Count the keys tied at the peak (the forward leaves Nmax to the backward): one sweep of
@@ -168,11 +167,11 @@ __global__ __launch_bounds__(64) void f32_bwd_dq_kernel(BwdParams p) {
       nmax += (sv > 0.f ? sv : 0.f) == rM ? 1 : 0;
     }
   }
-  const float rG = nmax > 0 ? rcp[4] / (float)nmax : 0.f;
+  const float rG = nmax > 0 ? rcp[6] / (float)nmax : 0.f;  // du share of a tied key
   __syncthreads();
-  if (has) rcp[4] = rG;  // read by the dK/dV kernel
+  if (has) rcp[4] = rG * p.scale;  // dS share, read by the dK/dV kernel
   const int grp = row >> 5;
-  double dsum = 0.0;  // this row's sum of ds; per-tile fp32 sums are added in fp64
+  double dsum = 0.0;  // this row's sum of du; per-tile fp32 sums are added in fp64
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = t * TB;
     __syncthreads();
@@ -195,9 +194,10 @@ __global__ __launch_bounds__(64) void f32_bwd_dq_kernel(BwdParams p) {
       const float u = sv > 0.f ? sv : 0.f;
       const float u2 = u * u, u4 = u2 * u2;
       const float u9 = u4 * u4 * u;
-      float ds = rcoef * u9 * (dw - rD);
-      if (u == rM && u > 0.f) ds += rG;
-      tsum += ds;
+      float du = rcoef * u9 * (dw - rD);
+      if (u == rM && u > 0.f) du += rG;
+      tsum += du;
+      const float ds = du * p.scale;
 #pragma unroll
       for (int d = 0; d < D; ++d) dq[d] = __builtin_fmaf(ds, Ks[j][d], dq[d]);
     }
@@ -282,7 +282,8 @@ __global__ __launch_bounds__(64) void f32_bwd_dkdv_kernel(BwdParams p) {
   }
 }
 
-__global__ __launch_bounds__(256) void f32_dtau_kernel(const double* partials, int64_t n, float scale,
+// dtau = -(sum of the du partials), in fp64 and a fixed order.
+__global__ __launch_bounds__(256) void f32_dtau_kernel(const double* partials, int64_t n,
                                                        float* dtau) {
   __shared__ double red[256];
   double acc = 0.0;
@@ -293,7 +294,7 @@ __global__ __launch_bounds__(256) void f32_dtau_kernel(const double* partials, i
     if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
     __syncthreads();
   }
-  if (threadIdx.x == 0) dtau[0] = (float)(-red[0] / (double)scale);
+  if (threadIdx.x == 0) dtau[0] = (float)(-red[0]);
 }
 
 template <int D>
@@ -325,7 +326,7 @@ int bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, hipStrea
     if (causal) hipLaunchKernelGGL((f32_bwd_dq_kernel<D, true>), grid, block, 0, st, bp);
     else hipLaunchKernelGGL((f32_bwd_dq_kernel<D, false>), grid, block, 0, st, bp);
     hipLaunchKernelGGL(f32_dtau_kernel, dim3(1), dim3(256), 0, st, bp.partials,
-                       (int64_t)bp.B * bp.H * nb, bp.scale, bp.dtau);
+                       (int64_t)bp.B * bp.H * nb, bp.dtau);
     const int rc = launch_status("pnfx_flash_bwd(f32 dq)");
     if (rc) return rc;
   }

@@ -11,11 +11,16 @@ this module                    reference                                   lines
 The reference names ``triton_causal_fir`` / ``triton_pn_fir_tau_scores`` are
 kept as aliases so call sites can switch imports without edits.
 
-Dispatch follows the reference's rule, with the HIP kernels covering a wider
-range: GPU tensors always run the HIP kernels (FIR: any channel count and
-K <= 16 taps; row scores: any row length); CPU tensors take the eager
-primitives, as the reference does for non-CUDA tensors (:687, :797).  Flash
-attention has no CPU path in the reference and none here.
+Dispatch follows the reference's rules.  The FIR runs the HIP kernel exactly
+where the reference runs its Triton kernel -- a GPU tensor, K == 7 taps and at
+most 1024 channels (:687) -- and the eager ``causal_fir`` everywhere else, as
+the reference does: that eager path casts the taps to x's dtype (bf16-rounded
+taps for bf16 input), where the kernel keeps fp32 taps.  (Other tap counts up to
+16 and any channel count are available from the kernel directly, as
+``torch.ops.pnfx.fir_fwd``.)  Row scores run the HIP kernel for every GPU tensor
+(the reference stops at N = 4096, :797; the kernel has no such limit) and the
+eager composition for CPU tensors.  Flash attention has no CPU path in the
+reference and none here.
 """
 from __future__ import annotations
 
@@ -26,24 +31,22 @@ import torch
 from . import ops  # noqa: F401  (registers the pnfx:: ops)
 from .pnfirtau_attention import causal_fir, power_norm_peak_gate
 
-FIR_MAX_TAPS = 16
+FIR_KERNEL_TAPS = 7  # the reference's kernel path (src/triton_pnfirtau.py:687)
+FIR_KERNEL_MAX_C = 1024
 
 
 def hip_causal_fir(x: torch.Tensor, taps: torch.Tensor) -> torch.Tensor:
     """Causal depthwise FIR along N for x [B, N, C] (any strides), taps [K] oldest lag first.
 
-    GPU: HIP streaming kernel, fp32 taps and fp32 fused multiply-add chain in lag
-    order, one rounding to x's dtype (src/triton_pnfirtau.py:40-135).  Returns a
-    contiguous [B, N, C] tensor; backward is the adjoint FIR (taps get no grad).
+    GPU, K == 7, C <= 1024: the HIP streaming kernel -- fp32 taps and an fp32 fused
+    multiply-add chain in lag order, one rounding to x's dtype
+    (src/triton_pnfirtau.py:40-135); returns a contiguous [B, N, C] tensor, backward is
+    the adjoint FIR (taps get no grad).  Otherwise the eager ``causal_fir``
+    (src/triton_pnfirtau.py:685-691): CPU tensors, other tap counts, wider rows.
     """
-    if not x.is_cuda:
-        return causal_fir(x, taps)
-    K = taps.numel()
-    if K > FIR_MAX_TAPS:
-        raise NotImplementedError(f"hip_causal_fir: {K} taps > {FIR_MAX_TAPS}")
-    if K <= 1:
-        return x  # as the eager primitive (src/pnfirtau_attention.py:69-70)
-    return torch.ops.pnfx.fir_fwd(x, taps.reshape(-1))
+    if x.is_cuda and taps.numel() == FIR_KERNEL_TAPS and x.shape[-1] <= FIR_KERNEL_MAX_C:
+        return torch.ops.pnfx.fir_fwd(x, taps.reshape(-1))
+    return causal_fir(x, taps)
 
 
 def hip_causal_fir_heads(k: torch.Tensor, taps: torch.Tensor) -> torch.Tensor:
@@ -85,6 +88,10 @@ def hip_pn_fir_tau_scores(
 def _flash_attention(q, k, v, score_tau, scale, gamma, causal_mask, o_bnhd=False):
     if not q.is_cuda:
         raise RuntimeError("flash_pn_fir_tau_attention runs on the GPU only (as in the reference)")
+    # The reference's kernel types each operand separately; the HIP kernels take one dtype,
+    # so k and v are brought to q's (autograd casts their gradients back).
+    k = k if k.dtype == q.dtype else k.to(q.dtype)
+    v = v if v.dtype == q.dtype else v.to(q.dtype)
     has_gamma = gamma is not None and gamma > 0.0
     o = torch.ops.pnfx.flash_fwd(q, k, v, score_tau, float(scale),
                                  float(gamma) if has_gamma else 0.0, has_gamma,
@@ -114,10 +121,22 @@ def flash_pn_fir_tau_attention(
 
 def flash_pn_fir_tau_attention_with_stats(q, k_tilde, v, score_tau, scale=None, gamma=0.5,
                                           causal_mask=True):
-    """Forward only: (O, M, Z, Nmax, tile_mask) -- the saved statistics and the silence map."""
+    """Forward only: (O, M, Z, Nmax, tile_mask) -- the saved statistics and the silence map.
+
+    M is the row peak of u = relu(q k^T scale - tau), Nmax its tie count.  Z is the
+    normaliser O is divided by: the sum of P = u^10 plus 1e-12.  For bf16 inputs P is
+    rounded to bf16 before it weights V (as the reference's kernel does,
+    src/triton_pnfirtau.py:417-420), and Z sums exactly those rounded values -- so O is a
+    convex combination of the rows of V scaled by the gate; the reference's kernel sums the
+    unrounded fp32 P instead (:405, :422), which differs from this Z by the rounding of
+    the P terms (a relative 2^-8 at most, and far less on rows with many comparable
+    terms).  For fp32 inputs both sum the fp32 P.
+    """
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     has_gamma = gamma is not None and gamma > 0.0
+    k_tilde = k_tilde if k_tilde.dtype == q.dtype else k_tilde.to(q.dtype)
+    v = v if v.dtype == q.dtype else v.to(q.dtype)
     o, _, M, Z, Nm, mask = torch.ops.pnfx.flash_fwd(q, k_tilde, v, score_tau, float(scale),
                                                    float(gamma) if has_gamma else 0.0, has_gamma,
                                                    bool(causal_mask), False, True)

@@ -122,7 +122,9 @@ def pn_rows_fwd(raw: Tensor, tau: Tensor, scale: float, p: float, gamma: float, 
 def _(raw, tau, scale, p, gamma, has_gamma, causal):
     R = raw.numel() // max(raw.shape[-1], 1)
     f = lambda dt: torch.empty(R, device=raw.device, dtype=dt)  # noqa: E731
-    return torch.empty_like(raw), f(torch.float32), f(torch.float32), f(torch.int32)
+    # contiguous, as the real kernel returns it whatever raw's strides
+    w = torch.empty(raw.shape, dtype=raw.dtype, device=raw.device)
+    return w, f(torch.float32), f(torch.float32), f(torch.int32)
 
 
 @torch.library.custom_op("pnfx::pn_rows_bwd", mutates_args=(), device_types="cuda")
@@ -148,7 +150,8 @@ def pn_rows_bwd(dw: Tensor, raw: Tensor, tau: Tensor, M: Tensor, Z: Tensor, Nmax
 @pn_rows_bwd.register_fake
 def _(dw, raw, tau, M, Z, Nmax, scale, p, gamma, has_gamma, causal):
     R = raw.numel() // max(raw.shape[-1], 1)
-    return torch.empty_like(raw), torch.empty(R, device=raw.device, dtype=torch.float32)
+    return (torch.empty(raw.shape, dtype=raw.dtype, device=raw.device),
+            torch.empty(R, device=raw.device, dtype=torch.float32))
 
 
 def _rows_setup(ctx, inputs, output):
@@ -184,6 +187,30 @@ def _bhnd(t: Tensor, name: str, bf16: bool) -> Tensor:
     return t if ok else t.contiguous()
 
 
+def _check_qkv(q: Tensor, k: Tensor, v: Tensor) -> None:
+    """q, k and v must agree in shape, dtype and device: the kernels read all three with
+    q's element size.  (The Python entry points cast k and v to q's dtype first.)"""
+    for name, t in (("k", k), ("v", v)):
+        if t.shape != q.shape:
+            raise ValueError(f"flash: {name} has shape {tuple(t.shape)}, q has {tuple(q.shape)}")
+        if t.dtype != q.dtype:
+            raise TypeError(f"flash: {name} is {t.dtype}, q is {q.dtype}")
+        if t.device != q.device:
+            raise ValueError(f"flash: {name} is on {t.device}, q on {q.device}")
+
+
+# Above this sequence length the forward does not record the silence map (its
+# B*H*ceil(N/32)*ceil(N/64) bytes grow as N^2/2048 per (b, h)); the backward then
+# recomputes every causal tile.
+MASK_MAX_N = 65536
+
+
+def _mask_shape(B: int, H: int, N: int) -> tuple[int, int, int]:
+    if N > MASK_MAX_N:
+        return (0, 0, 0)
+    return (B * H, (N + 31) // 32, (N + 63) // 64)
+
+
 def _ptr4(t: Tensor) -> tuple[int, int, int, int]:
     """(data pointer, batch, head, row strides) of a [B,H,N,D] operand for the C ABI."""
     return t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)
@@ -212,8 +239,12 @@ def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma:
     fp32) is O's bf16 rounding residual, saved for an accurate backward.
     Nmax (peak-tie counts) is formed only with_nmax, else returned empty: the
     backward does not need it.  tile_mask is uint8 [B*H, ceil(N/32), ceil(N/64)]
-    (32-query x 64-key sub-tile activity).
+    (32-query x 64-key sub-tile activity): N^2/2048 bytes per (b, h), the one part of
+    the saved state that is not O(N); past MASK_MAX_N it is not formed (shape (0, 0, 0))
+    and the backward recomputes every causal tile.  k and v must have q's shape, dtype and
+    device.
     """
+    _check_qkv(q, k, v)
     B, H, N, D = q.shape
     code = _code(q, "flash")
     bf = code == _lib.PNFX_BF16
@@ -223,19 +254,20 @@ def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma:
     M = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     Z = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     Nm = torch.empty((B, H, N) if with_nmax else (0,), device=q.device, dtype=torch.int32)
-    # one allocation: the tile mask, then (256-byte aligned) the workspace of the silent-tile
-    # bound (per-tile key norms, a few KiB)
-    mshape = (B * H, (N + 31) // 32, (N + 63) // 64)
-    mbytes = (mshape[0] * mshape[1] * mshape[2] + 255) // 256 * 256
+    # one allocation: the tile mask (N^2/2048 bytes per (b, h); none past MASK_MAX_N), then
+    # (256-byte aligned) the workspace of the silent-tile bound (per-tile key norms, a few KiB)
+    mshape = _mask_shape(B, H, N)
+    mn = mshape[0] * mshape[1] * mshape[2]
+    mbytes = (mn + 255) // 256 * 256
     nws = _fwd_workspace_bytes(B, H, N, D)
     buf = torch.empty(mbytes + nws, device=q.device, dtype=torch.uint8)
-    mask = buf[:mshape[0] * mshape[1] * mshape[2]].view(mshape)
+    mask = buf[:mn].view(mshape)
     ws = buf[mbytes:]
     t32 = _tau32(tau)
     rc = _lib.lib().pnfx_flash_fwd(
         *_ptr4(q), *_ptr4(k), *_ptr4(v), *_ptr4(o), o_lo.data_ptr() if bf else None,
-        M.data_ptr(), Z.data_ptr(), Nm.data_ptr() if with_nmax else None, mask.data_ptr(),
-        ws.data_ptr(), nws, B, H, N, D,
+        M.data_ptr(), Z.data_ptr(), Nm.data_ptr() if with_nmax else None,
+        mask.data_ptr() if mn else None, ws.data_ptr() if nws else None, nws, B, H, N, D,
         t32.data_ptr(), scale, gamma, int(has_gamma), int(causal), code, _stream(q))
     _lib.check(rc, "pnfx_flash_fwd")
     return o, o_lo, M, Z, Nm, mask
@@ -248,7 +280,7 @@ def _(q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd, with_nmax):
     o_lo = _new_o(q, o_bnhd) if q.dtype == torch.bfloat16 else q.new_empty(0)
     f = lambda dt: q.new_empty((B, H, N), dtype=dt)  # noqa: E731
     nm = q.new_empty((B, H, N) if with_nmax else (0,), dtype=torch.int32)
-    mask = q.new_empty((B * H, (N + 31) // 32, (N + 63) // 64), dtype=torch.uint8)
+    mask = q.new_empty(_mask_shape(B, H, N), dtype=torch.uint8)
     return o, o_lo, f(torch.float32), f(torch.float32), nm, mask
 
 
@@ -257,6 +289,10 @@ def flash_bwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, o: Tensor, o_lo: Ten
               M: Tensor, Z: Tensor, mask: Tensor, scale: float, gamma: float,
               has_gamma: bool, causal: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Deterministic flash backward; returns (dq, dk, dv, dtau) with dtau a 1-element fp32 tensor."""
+    _check_qkv(q, k, v)
+    if o.shape != q.shape or do.shape != q.shape:
+        raise ValueError(f"flash_bwd: o {tuple(o.shape)} / dO {tuple(do.shape)} must match q "
+                         f"{tuple(q.shape)}")
     B, H, N, D = q.shape
     code = _code(q, "flash")
     bf = code == _lib.PNFX_BF16
@@ -276,7 +312,7 @@ def flash_bwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, o: Tensor, o_lo: Ten
     t32 = _tau32(tau)
     rc = L.pnfx_flash_bwd(
         *_ptr4(q), *_ptr4(k), *_ptr4(v), *_ptr4(o), o_lo.data_ptr() if use_lo else None,
-        *_ptr4(do), M.data_ptr(), Z.data_ptr(), mask.data_ptr(),
+        *_ptr4(do), M.data_ptr(), Z.data_ptr(), mask.data_ptr() if mask.numel() else None,
         *_ptr4(dq), *_ptr4(dk), *_ptr4(dv), dtau.data_ptr(), ws.data_ptr(), ws_bytes, B, H, N, D,
         t32.data_ptr(), scale, gamma, int(has_gamma), int(causal), code, _stream(q))
     _lib.check(rc, "pnfx_flash_bwd")

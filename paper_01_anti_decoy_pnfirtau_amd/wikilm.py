@@ -105,6 +105,21 @@ class WikiLM(nn.Module):
         return self.head(self.ln_f(h))
 
 
+def zipf_tokens(batch: int, seq: int, vocab: int, seed: int, s: float = 1.1) -> torch.Tensor:
+    """Synthetic token ids [batch, seq] ~ Zipf(s) truncated to [0, vocab) by rejection,
+    seeded on the CPU (the benchmark LM workload: no dataset is fetched)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    need, out = batch * seq, []
+    while need > 0:
+        z = rng.zipf(s, size=2 * need) - 1
+        z = z[z < vocab][:need]
+        out.append(z)
+        need -= len(z)
+    return torch.from_numpy(np.concatenate(out).reshape(batch, seq).astype(np.int64))
+
+
 def make_optimizer(model: nn.Module, cfg: WikiLMConfig, capturable: bool = False,
                    fused: bool | None = None):
     """AdamW as the reference builds it (experiments/exp4_wikitext2_lm.py:326-328).
@@ -139,13 +154,22 @@ class GraphedStep:
 
     Gradients are cleared by a fill kernel inside the graph (``zero_grad`` with
     ``set_to_none=False``) rather than by dropping the tensors, so the captured addresses stay
-    valid; the optimizer must be built with ``capturable=True``.  ``x`` is a static input:
-    copy new tokens into it before ``replay``.  The loss of the last replay is ``self.loss``.
+    valid; the optimizer must be built with ``capturable=True`` and have no state yet.  ``x``
+    is a static input: copy new tokens into it before ``replay``.  The loss of the last replay
+    is ``self.loss``.
+
+    Construction runs ``warmup`` real steps on ``x`` (the allocator and the optimizer's state
+    must exist before capture), then puts every parameter and buffer back and zeroes the
+    optimizer state in place (for Adam-type optimizers a zero state, step count included, is
+    the fresh state): the first ``replay`` is the model's first training step.
     """
 
     def __init__(self, model: nn.Module, opt: torch.optim.Optimizer, x: torch.Tensor,
                  amp: bool = True, warmup: int = 3):
         self.model, self.opt, self.x, self.amp = model, opt, x, amp
+        if any(len(st) for st in opt.state.values()):
+            raise ValueError("GraphedStep: the optimizer already has state")
+        saved = [t.detach().clone() for t in list(model.parameters()) + list(model.buffers())]
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -155,6 +179,15 @@ class GraphedStep:
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self.loss = self._step()
+        # capture records the step without running it: undo the warm-up steps in place, so
+        # the captured addresses stay the live ones
+        with torch.no_grad():
+            for t, s in zip(list(model.parameters()) + list(model.buffers()), saved):
+                t.copy_(s)
+            for st in opt.state.values():
+                for v in st.values():
+                    if torch.is_tensor(v):
+                        v.zero_()
 
     def _step(self) -> torch.Tensor:
         self.opt.zero_grad(set_to_none=False)

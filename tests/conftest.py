@@ -27,3 +27,17 @@ def golden(name):
     import numpy as np
 
     return np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False)
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """Write the recorded parity ratios to $PNFX_PARITY_REPORT (JSON), if that is set."""
+    path = os.environ.get("PNFX_PARITY_REPORT")
+    if not path:
+        return
+    import json
+
+    from tests.helpers import PARITY_LOG
+
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    with open(path, "w") as f:
+        json.dump(PARITY_LOG, f, indent=0)

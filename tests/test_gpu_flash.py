@@ -1,10 +1,10 @@
 """GPU parity of the flash forward/backward against the float64 oracle.
 
-Tolerances: bf16 inputs -- rtol 2e-2 / atol 2e-3 as tests.helpers.assert_bf16_close
-states them (max and mean error relative to the tensor's scale), against the oracle
-evaluated in float64 on the same bf16-rounded inputs; fp32 inputs -- every element
-within 1e-5 of the tensor's scale.  dtau is a sum with cancellation: its bound is
-taken relative to |dtau| + sum|du|.
+Tolerances: bf16 inputs -- every element within 2e-3 max|ref| + 2e-2 |ref|
+(tests.helpers.assert_bf16_close: rtol 2e-2, atol 2e-3 of the tensor's scale), against
+the oracle evaluated in float64 on the same bf16-rounded inputs; fp32 inputs -- every
+element within 1e-5 max|ref| + 1e-5 |ref|.  dtau is a sum with cancellation: its bound
+is taken relative to |dtau| + sum|du|.
 """
 import numpy as np
 import pytest
@@ -15,7 +15,8 @@ from paper_01_anti_decoy_pnfirtau_amd.hip_pnfirtau import (flash_pn_fir_tau_atte
                                                            flash_pn_fir_tau_attention_with_stats,
                                                            tile_mask_64)
 from tests.helpers import (BF16_ATOL, BF16_RTOL, F32_TOL, assert_bf16_close, assert_close,
-                           assert_sum_close, flash_oracle, seeded, to_np64)
+                           assert_sum_close, flash_oracle, flash_reference_rounding, seeded,
+                           to_np64)
 
 pytestmark = pytest.mark.gpu
 
@@ -58,13 +59,105 @@ def test_flash_matches_oracle(dev, dtype, B, H, N, D, tau, gamma, causal):
     dO = seeded((B, H, N, D), 23, dtype, dev)
     o, dq, dk, dv, dtau = _run(q, k, v, tau, dO, scale, gamma, causal)
     Of, M, Z, Nm, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, tau, dO, scale, gamma, causal)
+    em = flash_reference_rounding(q, k, v, tau, dO, scale, gamma, causal)
     for name, got, want in (("O", o, Of), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
         if dtype == torch.bfloat16:
-            assert_bf16_close(to_np64(got), want, name)
+            assert_bf16_close(to_np64(got), want, name, em.get(name))
         else:
             assert_close(to_np64(got), want, F32_TOL, F32_TOL, name)
     tol = BF16_ATOL if dtype == torch.bfloat16 else F32_TOL
     assert_sum_close(float(dtau), rdt, dabs, tol, "dtau")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,H,N,D,tau,gamma,causal", CASES)
+def test_flash_stats_match_oracle(dev, dtype, B, H, N, D, tau, gamma, causal):
+    """The saved statistics: M (row peak) and Nmax exactly as the oracle's up to the inputs'
+    rounding; Z = sum of the P that weight V + 1e-12 -- for bf16 the bf16-rounded P (oracle
+    with p_bf16, fp32 summation order aside), which is within the bf16 bar of the exact
+    sum; for fp32 the exact sum."""
+    scale = 1.0 / np.sqrt(D)
+    q = seeded((B, H, N, D), 20, dtype, dev)
+    k = seeded((B, H, N, D), 21, dtype, dev)
+    v = seeded((B, H, N, D), 22, dtype, dev)
+    t = torch.tensor(tau, device=dev)
+    o, M, Z, Nm, _ = flash_pn_fir_tau_attention_with_stats(q, k, v, t, scale=scale, gamma=gamma,
+                                                           causal_mask=causal)
+    qn, kn, vn = to_np64(q), to_np64(k), to_np64(v)
+    Of, Mo, Zo, No = O.flash_fwd(qn, kn, vn, tau, scale, gamma, causal)
+    tol = 1e-5
+    assert_close(to_np64(M), Mo, tol, tol, "M")  # M = s - tau can cancel: atol of the scale
+    if dtype == torch.bfloat16:
+        # Z sums the bf16-rounded P: it matches that sum to fp32 rounding on (nearly) every
+        # row -- a term whose fp32 and float64 values round to different bf16 neighbours
+        # moves a row by one bf16 step of that term -- and the exact sum within the bf16 bar
+        _, _, Zb, _ = O.flash_fwd(qn, kn, vn, tau, scale, gamma, causal, p_bf16=True)
+        zg = to_np64(Z)
+        assert np.mean(np.abs(zg - Zb) <= tol * Zb) >= 0.99
+        assert np.all(np.abs(zg - Zb) <= 2.0**-8 * Zb + tol * Zb)
+        assert_bf16_close(zg, Zo, "Z vs exact sum")
+    else:
+        assert_close(to_np64(Z), Zo, tol, 0.0, "Z")
+    assert np.array_equal(Nm.cpu().numpy(), No)
+
+
+def test_flash_negative_scale_with_tau_matches_oracle(dev):
+    """A negative score scale with tau > 0 on the default (bounded, bf16, d = 64) path: the
+    silent-tile bound uses |scale|, so it only skips tiles that are silent."""
+    B, H, N, D = 1, 2, 300, 64
+    q = seeded((B, H, N, D), 90, torch.bfloat16, dev)
+    k = seeded((B, H, N, D), 91, torch.bfloat16, dev)
+    v = seeded((B, H, N, D), 92, torch.bfloat16, dev)
+    dO = seeded((B, H, N, D), 93, torch.bfloat16, dev)
+    scale, tau = -0.125, 0.2
+    o, dq, dk, dv, dtau = _run(q, k, v, tau, dO, scale, 0.5, True)
+    Of, M, Z, Nm, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, tau, dO, scale, 0.5, True)
+    em = flash_reference_rounding(q, k, v, tau, dO, scale, 0.5, True)
+    assert np.abs(Of).max() > 0.1
+    for name, got, want in (("O", o, Of), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert_bf16_close(to_np64(got), want, name, em.get(name))
+    assert_sum_close(float(dtau), rdt, dabs, BF16_ATOL, "dtau")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_flash_zero_scale_gives_finite_dtau(dev, dtype):
+    """scale = 0: every score is -tau; with tau < 0 every causal key ties at the peak.  dS =
+    du * scale is 0, so dQ = dK = 0, while dtau = -sum du stays finite and equals the
+    oracle's."""
+    B, H, N, D = 1, 1, 100, 64
+    q = seeded((B, H, N, D), 94, dtype, dev)
+    k = seeded((B, H, N, D), 95, dtype, dev)
+    v = seeded((B, H, N, D), 96, dtype, dev)
+    dO = seeded((B, H, N, D), 97, dtype, dev)
+    o, dq, dk, dv, dtau = _run(q, k, v, -0.3, dO, 0.0, 0.5, True)
+    Of, M, Z, Nm, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, -0.3, dO, 0.0, 0.5, True)
+    em = flash_reference_rounding(q, k, v, -0.3, dO, 0.0, 0.5, True)
+    assert np.isfinite(float(dtau))
+    assert torch.all(dq == 0) and torch.all(dk == 0)
+    tol = BF16_ATOL if dtype == torch.bfloat16 else F32_TOL
+    assert_sum_close(float(dtau), rdt, dabs, tol, "dtau")
+    if dtype == torch.bfloat16:
+        assert_bf16_close(to_np64(dv), rdv, "dv", em.get("dv"))
+    else:
+        assert_close(to_np64(dv), rdv, F32_TOL, F32_TOL, "dv")
+
+
+def test_flash_mixed_input_dtypes_follow_q(dev):
+    """k and v of another dtype than q are cast to q's (the kernels take one element type);
+    their gradients come back in their own dtype."""
+    B, H, N, D = 1, 2, 130, 64
+    q = seeded((B, H, N, D), 98, torch.bfloat16, dev)
+    k32 = seeded((B, H, N, D), 99, torch.float32, dev)
+    v = seeded((B, H, N, D), 100, torch.bfloat16, dev)
+    dO = seeded((B, H, N, D), 101, torch.bfloat16, dev)
+    kb = k32.to(torch.bfloat16)
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k32, v))
+    tau = torch.tensor(0.0, device=dev)
+    o1 = flash_pn_fir_tau_attention(qa, ka, va, tau)
+    o1.backward(dO)
+    o2, dq2, dk2, dv2, _ = _run(q, kb, v, 0.0, dO, None, 0.5, True)
+    assert torch.equal(o1, o2) and torch.equal(qa.grad, dq2)
+    assert ka.grad.dtype == torch.float32 and torch.equal(ka.grad, dk2.float())
 
 
 # bf16 kernels fold a power-of-two scale into the operands and -tau into the MFMA
@@ -83,8 +176,9 @@ def test_flash_scale_paths(dev, D, scale):
     dO = seeded((B, H, N, D), 27, torch.bfloat16, dev)
     o, dq, dk, dv, dtau = _run(q, k, v, 0.1, dO, scale, 0.5, True)
     Of, M, Z, Nm, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, 0.1, dO, scale, 0.5, True)
+    em = flash_reference_rounding(q, k, v, 0.1, dO, scale, 0.5, True)
     for name, got, want in (("O", o, Of), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
-        assert_bf16_close(to_np64(got), want, name)
+        assert_bf16_close(to_np64(got), want, name, em.get(name))
     assert_sum_close(float(dtau), rdt, dabs, BF16_ATOL, "dtau")
 
 
@@ -103,13 +197,14 @@ def test_flash_stats_and_planted_ties(dev, dtype, scale):
     o, M, Z, Nm, mask = flash_pn_fir_tau_attention_with_stats(q, k, v, torch.tensor(0.0, device=dev),
                                                               scale=scale)
     Of, Mo, Zo, No, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, 0.0, dO, scale, 0.5, True)
+    em = flash_reference_rounding(q, k, v, 0.0, dO, scale, 0.5, True)
     assert (No[:, :, 160:] == 3).all()
     assert np.array_equal(Nm.cpu().numpy()[:, :, 160:], No[:, :, 160:])
     np.testing.assert_allclose(M.cpu().numpy(), Mo, rtol=1e-2 if dtype == torch.bfloat16 else 1e-5)
     _, dq, dk, dv, dtau = _run(q, k, v, 0.0, dO, scale, 0.5, True)
     for name, got, want in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
         if dtype == torch.bfloat16:
-            assert_bf16_close(to_np64(got), want, name)
+            assert_bf16_close(to_np64(got), want, name, em.get(name))
         else:
             assert_close(to_np64(got), want, F32_TOL, F32_TOL, name)
     tol = BF16_ATOL if dtype == torch.bfloat16 else F32_TOL
@@ -128,12 +223,13 @@ def test_flash_rows_with_every_key_tied(dev, dtype):
     tau = -0.2
     o, M, Z, Nm, mask = flash_pn_fir_tau_attention_with_stats(q, k, v, torch.tensor(tau, device=dev))
     Of, Mo, Zo, No, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, tau, dO, 1 / 8, 0.5, True)
+    em = flash_reference_rounding(q, k, v, tau, dO, 1 / 8, 0.5, True)
     assert np.array_equal(No[0, 0, 100:], np.arange(101, N + 1))
     assert np.array_equal(Nm.cpu().numpy(), No)
     o, dq, dk, dv, dtau = _run(q, k, v, tau, dO, 1 / 8, 0.5, True)
     for name, got, want in (("O", o, Of), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
         if dtype == torch.bfloat16:
-            assert_bf16_close(to_np64(got), want, name)
+            assert_bf16_close(to_np64(got), want, name, em.get(name))
         else:
             assert_close(to_np64(got), want, F32_TOL, F32_TOL, name)
     tol = BF16_ATOL if dtype == torch.bfloat16 else F32_TOL
@@ -197,8 +293,9 @@ def test_flash_gradients_with_silent_key_tiles(dev, N, D, causal, pattern):
     scale = 1.0 / np.sqrt(D)
     o, dq, dk, dv, dtau = _run(q, k, v, 0.25, dO, scale, 0.5, causal)
     Of, M, Z, Nm, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, 0.25, dO, scale, 0.5, causal)
+    em = flash_reference_rounding(q, k, v, 0.25, dO, scale, 0.5, causal)
     for name, got, want in (("O", o, Of), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
-        assert_bf16_close(to_np64(got), want, name)
+        assert_bf16_close(to_np64(got), want, name, em.get(name))
     # silent key blocks get exactly zero dK and dV
     for j in blocks:
         assert torch.all(dk[:, :, 64 * j:64 * j + 64] == 0) and torch.all(dv[:, :, 64 * j:64 * j + 64] == 0)
@@ -357,28 +454,44 @@ def test_flash_strided_inputs_match_contiguous(dev):
 
 
 FULL = [
-    # name, B, H, N, D, input std, checked (b, h) slice
-    ("C4", 4, 16, 8192, 64, 1.0, (2, 5)),
-    ("C5", 8, 8, 4096, 128, 128 ** -0.25, (7, 3)),
+    # name, B, H, N, D, input std, tau, planted silent key blocks, checked (b, h) slice
+    ("C4", 4, 16, 8192, 64, 1.0, 0.0, False, (2, 5)),
+    ("C4_silent50", 4, 16, 8192, 64, 1.0, 0.25, True, (1, 7)),
+    ("C5", 8, 8, 4096, 128, 128 ** -0.25, 0.0, False, (7, 3)),
 ]
 
 
-@pytest.mark.parametrize("name,B,H,N,D,std,bh", FULL)
-def test_flash_full_size_slice_matches_oracle(dev, name, B, H, N, D, std, bh):
-    """At the benchmark shapes: the whole batch runs on the GPU; one (b, h) slice of O, dQ, dK
-    and dV is checked against the float64 oracle on the same bf16 inputs (the slices are
-    independent, so one slice exercises every tile position of the full-size launch)."""
-    print(f"[flash full {name} B={B} H={H} N={N} D={D}]", flush=True)
+@pytest.mark.parametrize("name,B,H,N,D,std,tau,silent,bh", FULL)
+def test_flash_full_size_slice_matches_oracle(dev, name, B, H, N, D, std, tau, silent, bh):
+    """At the benchmark shapes (C4 with tau = 0 and with 50 % of the causal 64x64 tiles
+    planted silent, C5): the whole batch runs on the GPU; one (b, h) slice of O, dQ, dK and
+    dV, its M and Z, and dtau are checked against the float64 oracle on the same bf16 inputs.
+    dO is zero outside the checked slice, so the global dtau is that slice's dtau (the
+    slices are independent: one slice exercises every tile position of the full launch)."""
+    print(f"[flash full {name} B={B} H={H} N={N} D={D} tau={tau}]", flush=True)
     g = torch.Generator().manual_seed(11)
     q, k, v, dO = [(torch.randn(B, H, N, D, generator=g) * std).to(torch.bfloat16).to(dev)
                    for _ in range(4)]
-    o, dq, dk, dv, _ = _run(q, k, v, 0.0, dO, None, 0.5, True)
+    if silent:
+        nb = N // 64
+        for j in range(0, nb, 2):
+            if j != 96:
+                k[:, :, 64 * j:64 * j + 64] = 0
     b, h = bh
+    keep = torch.zeros_like(dO)
+    keep[b, h] = dO[b, h]
+    dO = keep
+    o, dq, dk, dv, dtau = _run(q, k, v, tau, dO, None, 0.5, True)
+    _, M, Z, _, _ = flash_pn_fir_tau_attention_with_stats(q, k, v, torch.tensor(tau, device=dev))
     scale = 1.0 / np.sqrt(D)
-    Of, _, _, _, rq, rk, rv, _, _ = flash_oracle(q[b, h], k[b, h], v[b, h], 0.0, dO[b, h], scale,
-                                                 0.5, True)
-    for what, got, want in (("O", o, Of), ("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
-        assert_bf16_close(to_np64(got[b, h]), want, f"{name} {what}")
+    Of, Mo, Zo, _, rq, rk, rv, rdt, dabs = flash_oracle(q[b, h], k[b, h], v[b, h], tau, dO[b, h],
+                                                        scale, 0.5, True)
+    em = flash_reference_rounding(q[b, h], k[b, h], v[b, h], tau, dO[b, h], scale, 0.5, True)
+    for what, got, want in (("O", o, Of), ("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        assert_bf16_close(to_np64(got[b, h]), want, f"{name} {what}", em[what])
+    assert_sum_close(float(dtau), rdt, dabs, BF16_ATOL, f"{name} dtau")
+    assert_close(to_np64(M[b, h]), Mo, 1e-5, 1e-5, f"{name} M")
+    assert_bf16_close(to_np64(Z[b, h]), Zo, f"{name} Z")
 
 
 def test_flash_full_size_gradients_scale_exactly_with_dout(dev):

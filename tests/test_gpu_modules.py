@@ -6,7 +6,8 @@ import torch
 import paper_01_anti_decoy_pnfirtau_amd as P
 from tests.conftest import golden
 from oracle import pnfirtau_oracle as O
-from tests.helpers import assert_bf16_close, assert_close, assert_sum_close, to_np64
+from tests.helpers import (PARITY_LOG, assert_bf16_close, assert_close, assert_sum_close, seeded,
+                           to_np64)
 from tests.test_package_cpu import _load_mha, _t
 
 pytestmark = pytest.mark.gpu
@@ -45,16 +46,93 @@ def test_flash_mha_return_weights_uses_row_path(dev):
     assert_close(to_np64(out), f["out"], 1e-5, 1e-5, "out")
 
 
-@pytest.mark.parametrize("cls", [P.PnFirTauFlashMHA, P.PnFirTauTritonMHA])
-def test_hip_mha_bf16_within_bf16_tolerance_of_reference(dev, cls):
-    """bf16 weights/activations vs the reference's fp32 result on the same bf16-rounded data."""
-    f = golden("c1_mha_fp32")
-    m = _load_mha(cls, f)
-    mb = _load_mha(cls, f).to(torch.bfloat16).to(dev)
-    x32 = _t(f["x"]).bfloat16().float()
-    ref = _load_mha(P.PnFirTauMHA, f)
-    for p_, pb in zip(ref.parameters(), mb.parameters()):
-        p_.data.copy_(pb.data.float().cpu())
-    yr = ref(x32)
-    yb = mb(_t(f["x"]).bfloat16().to(dev))
-    assert_bf16_close(to_np64(yb), to_np64(yr), "out")
+def test_hip_mha_bf16_error_vs_reference_bf16_path(dev):
+    """The HIP bf16 modules end to end (bf16 weights, bf16 projections) against the float64
+    oracle on the same bf16 weights and input, beside the reference's own bf16 result (its
+    eager PnFirTauMHA run in bf16, stored in the c1_mha_bf16 fixture): output and input
+    gradient within the bf16 bar, or -- where the bf16 projections alone take an element past
+    it -- no further past it than the reference's bf16 path goes (max error / scale too)."""
+    f = golden("c1_mha_bf16")
+    B, N, D, H, _ = [int(v) for v in f["meta"]]
+    g = float(f["gamma"])
+    r = O.mha_fwd_bwd(to_np64(_t(f["x"])), to_np64(_t(f["w_qkv"])), to_np64(_t(f["w_out"])),
+                      float(f["tau"]), to_np64(_t(f["taps"])), H, dout=to_np64(_t(f["dout"])),
+                      gamma=None if np.isnan(g) else g)
+    ref_err = {k: np.abs(to_np64(_t(f[k])) - r[k]).max() / np.abs(r[k]).max() for k in ("out", "dx")}
+    for cls in (P.PnFirTauFlashMHA, P.PnFirTauTritonMHA):
+        m = _load_mha(cls, f, dtype=torch.bfloat16).to(dev)
+        x = _t(f["x"]).to(dev).requires_grad_(True)
+        out = m(x)
+        out.backward(_t(f["dout"]).to(dev))
+        torch.cuda.synchronize()
+        for key, t in (("out", out), ("dx", x.grad)):
+            got = to_np64(t)
+            assert_bf16_close(got, r[key], f"{cls.__name__} {key}", to_np64(_t(f[key])))
+            err = np.abs(got - r[key]).max() / np.abs(r[key]).max()
+            print(f"[{cls.__name__} {key}] max err / scale: HIP bf16 {err:.3g}, "
+                  f"reference bf16 {ref_err[key]:.3g}", flush=True)
+            assert err <= ref_err[key] * 1.25 + 2e-3
+
+
+def test_reference_fp32_parity_protocol(dev):
+    """The reference's published fp32 parity check (experiments/exp4_wikitext2_lm.py:385-455:
+    PnFirConfig(d_model=64, n_heads=4), B=8, N=128, TF32 off; the materialised-score and
+    flash modules against the eager PnFirTauMHA with the same state_dict and input) on the
+    GPU.  The reference reports max-abs out 2.38e-7, dx 1.32e-6, dtau 4.01e-5 for its flash
+    module on its own random draw (results/exp4_wikitext2_lm.json:122-143); here the same
+    statistics must stay within 1e-5 of the reference-norms (relative) and are printed."""
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        torch.manual_seed(0)
+        acfg = P.PnFirConfig(d_model=64, n_heads=4, dropout=0.0)
+        m_ref = P.PnFirTauMHA(acfg).to(dev)
+        mods = {"pn_fir_tau_triton": P.PnFirTauTritonMHA(acfg).to(dev),
+                "pn_fir_tau_flash": P.PnFirTauFlashMHA(acfg).to(dev)}
+        for m in mods.values():
+            m.load_state_dict(m_ref.state_dict())
+        g = torch.Generator().manual_seed(1)
+        x = torch.randn(8, 128, 64, generator=g).to(dev)
+        dy = torch.randn(8, 128, 64, generator=g).to(dev)
+        x1 = x.clone().requires_grad_(True)
+        y1 = m_ref(x1)
+        y1.backward(dy)
+        out_n, dx_n = float(y1.abs().max()), float(x1.grad.abs().max())
+        dtau_n = float(m_ref.score_tau.grad.abs())
+        for name, m in mods.items():
+            x2 = x.clone().requires_grad_(True)
+            y2 = m(x2)
+            y2.backward(dy)
+            torch.cuda.synchronize()
+            od = float((y1 - y2).abs().max())
+            dd = float((x1.grad - x2.grad).abs().max())
+            td = float((m_ref.score_tau.grad - m.score_tau.grad).abs())
+            PARITY_LOG.append({"test": "reference_fp32_parity_protocol", "what": name,
+                               "out_max_diff": od, "out_rel_diff": od / out_n,
+                               "dx_max_diff": dd, "dx_rel_diff": dd / dx_n,
+                               "dtau_diff": td, "dtau_rel_diff": td / max(dtau_n, 1e-12),
+                               "reference_norms": [out_n, dx_n, dtau_n]})
+            print(f"[fp32 parity {name}] out {od:.2e} (rel {od / out_n:.2e}) dx {dd:.2e} "
+                  f"(rel {dd / dx_n:.2e}) dtau {td:.2e} (rel {td / max(dtau_n, 1e-12):.2e})",
+                  flush=True)
+            assert od <= 1e-5 * out_n and dd <= 1e-5 * dx_n and td <= 1e-5 * max(dtau_n, 1.0)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+
+
+@pytest.mark.parametrize("K", [3, 5, 7, 9])
+def test_fir_dispatch_follows_reference(dev, K):
+    """triton_causal_fir's dispatch (src/triton_pnfirtau.py:685-691): the kernel for K == 7 and
+    C <= 1024, the eager causal_fir (x-dtype taps) otherwise -- so for K != 7 a bf16 input
+    gives bitwise the eager result, as in the reference."""
+    from paper_01_anti_decoy_pnfirtau_amd.hip_pnfirtau import hip_causal_fir
+
+    x = seeded((2, 70, 48), 5, torch.bfloat16, dev)
+    taps = P.causal_gaussian_taps(K)
+    y = hip_causal_fir(x, taps)
+    kernel = torch.ops.pnfx.fir_fwd(x, taps.to(dev))
+    eager = P.causal_fir(x, taps)
+    assert torch.equal(y, kernel if K == 7 else eager)
+    assert not torch.equal(kernel, eager)  # bf16 taps vs fp32 taps: the two paths differ
+    wide = seeded((1, 9, 1040), 6, torch.bfloat16, dev)  # C > 1024: eager for every K
+    assert torch.equal(hip_causal_fir(wide, taps), P.causal_fir(wide, taps))

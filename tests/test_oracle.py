@@ -223,6 +223,56 @@ def test_flash_special_cases():
     assert np.all(Of[0, 0, 0] == 0)
 
 
+def test_flash_bf16_weights_option_known_answers():
+    """p_bf16 rounds P = u^10 to bf16 before it weights v and enters Z.  One key with
+    u = 1.5: P = 1.5^10 = 57.665..., whose bf16 value is 231/128 * 32 = 57.75 (rounding u
+    instead of P would leave 57.665).  Powers of two are exact in bf16, so u in {0.5, 1, 2}
+    gives bitwise the unrounded result."""
+    q = np.ones((1, 1, 1, 1)); k = np.full((1, 1, 1, 1), 1.5); v = np.full((1, 1, 1, 1), 3.0)
+    Of, M, Z, Nm = O.flash_fwd(q, k, v, 0.0, 1.0, None, True, p_bf16=True)
+    assert Z[0, 0, 0] == 57.75 + 1e-12
+    assert abs(Of[0, 0, 0, 0] - 3.0 * 57.75 / (57.75 + 1e-12)) <= 1e-14
+    assert O.flash_fwd(q, k, v, 0.0, 1.0, None, True)[2][0, 0, 0] == 1.5**10 + 1e-12
+    q = np.ones((1, 1, 3, 1)); k = np.array([0.5, 1.0, 2.0]).reshape(1, 1, 3, 1)
+    v = np.arange(3.0).reshape(1, 1, 3, 1)
+    a = O.flash_fwd(q, k, v, 0.0, 1.0, 0.5, True, p_bf16=True)
+    b = O.flash_fwd(q, k, v, 0.0, 1.0, 0.5, True)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+    # on random rows the rounded mass stays within the bf16 rounding of its terms
+    rng = np.random.default_rng(9)
+    q, k, v = _rand_qkv(rng, 1, 2, 64, 8)
+    Zr = O.flash_fwd(q, k, v, 0.0, p_bf16=True)[2]
+    Ze = O.flash_fwd(q, k, v, 0.0)[2]
+    assert np.all(np.abs(Zr - Ze) <= 2.0**-8 * Ze)  # bf16 unit roundoff
+    assert np.any(Zr != Ze)
+
+
+def test_flash_reference_bf16_rounding_points_known_answers():
+    """One query, one key (d = 1, q = k = 1, v = 3, dO = 1, scale 1, tau 0, gamma 0.5): u = 1,
+    P = 1, g = 2/3, O = 2, D = <dO, O>/g = 3 = dW, so du is the tie term alone,
+    3 * 0.5 / 1.5^2 = 2/3.  The reference's kernels round dS = 2/3 and w = g/Z ~ 2/3 to bf16,
+    0.66796875 (= 171/256): dq = dk = dv = 0.66796875, while dtau = -2/3 is not rounded.
+    The float64 oracle gives 2/3 for all three."""
+    one = np.ones((1, 1, 1, 1))
+    O_, dq, dk, dv, dt = O.flash_reference_bf16(one, one, 3 * one, 0.0, one, 1.0, 0.5, True)
+    assert O_[0, 0, 0, 0] == 2.0
+    assert dq[0, 0, 0, 0] == dk[0, 0, 0, 0] == dv[0, 0, 0, 0] == 171 / 256
+    assert abs(dt + 2 / 3) < 1e-12
+    eq, ek, ev, et = O.flash_bwd(one, one, 3 * one, 0.0, one, 1.0, 0.5, True)
+    # (the 1e-12 in Z leaves dW - D = 3e-12, hence the 1e-10)
+    assert abs(eq[0, 0, 0, 0] - 2 / 3) < 1e-10 and abs(ek[0, 0, 0, 0] - 2 / 3) < 1e-10
+    assert abs(ev[0, 0, 0, 0] - 2 / 3) < 1e-10 and abs(et - dt) < 1e-10
+    # on random inputs it stays within bf16 rounding of the exact gradients
+    rng = np.random.default_rng(10)
+    q, k, v = _rand_qkv(rng, 1, 1, 48, 8)
+    d = rng.standard_normal(q.shape)
+    _, rq, rk, rv, rt = O.flash_reference_bf16(q, k, v, 0.0, d)
+    xq, xk, xv, xt = O.flash_bwd(q, k, v, 0.0, d)
+    for a, b in ((rq, xq), (rk, xk), (rv, xv)):
+        assert np.abs(a - b).max() <= 0.05 * np.abs(b).max() and np.any(a != b)
+
+
 def test_tile_activity_closed_form_all_active():
     # every causal tile active: fully-silent fraction of the nb^2 grid is (nb-1)/(2nb)
     # (0.46875 at nb = 16, the exp4b convention, results/exp4b_mha6_instrumentation.json:24-157)

@@ -180,3 +180,44 @@ def test_wikilm_variants_share_init_and_train_on_cpu():
     assert losses["pn_fir_tau"][1] < losses["pn_fir_tau"][0]
     with pytest.raises(ValueError):
         WikiLM(50, cfg, "softmax")
+
+
+def test_flash_op_checks_operand_agreement_on_the_host():
+    """k and v of another shape, dtype or device than q are refused before any kernel is
+    called (the kernels read all three with q's element size and extents)."""
+    from paper_01_anti_decoy_pnfirtau_amd import ops
+
+    q = torch.randn(1, 2, 8, 16)
+    ops._check_qkv(q, q.clone(), q.clone())
+    with pytest.raises(TypeError):
+        ops._check_qkv(q, q.to(torch.bfloat16), q)
+    with pytest.raises(ValueError):
+        ops._check_qkv(q, q, q[:, :, :4])
+    with pytest.raises(ValueError):
+        ops._check_qkv(q, q.to("meta"), q)
+
+
+def test_tile_mask_shape_and_its_length_limit():
+    """The forward's silence map is [B*H, ceil(N/32), ceil(N/64)] bytes -- N^2/2048 per (b, h) --
+    and is not formed past MASK_MAX_N (the backward then recomputes every tile)."""
+    from paper_01_anti_decoy_pnfirtau_amd import ops
+
+    assert ops._mask_shape(2, 3, 100) == (6, 4, 2)
+    assert ops._mask_shape(1, 1, ops.MASK_MAX_N) == (1, ops.MASK_MAX_N // 32, ops.MASK_MAX_N // 64)
+    assert ops._mask_shape(1, 1, ops.MASK_MAX_N + 1) == (0, 0, 0)
+
+
+@pytest.mark.parametrize("K", [1, 5, 7])
+def test_fir_entry_point_takes_eager_path_on_cpu(K):
+    """triton_causal_fir on a CPU tensor is the eager causal_fir (src/triton_pnfirtau.py:687-691),
+    bit for bit the reference's golden for K = 7 in fp32 and bf16."""
+    from paper_01_anti_decoy_pnfirtau_amd.hip_pnfirtau import triton_causal_fir
+
+    f = golden("fir_eager")
+    taps = {1: _t(f["taps1"]), 5: _t(f["taps5"]), 7: _t(f["taps"])}[K]
+    for x in (_t(f["x"]), _t(f["x_bf16"])):
+        assert torch.equal(triton_causal_fir(x, taps), P.causal_fir(x, taps))
+    if K == 7:
+        assert torch.equal(triton_causal_fir(_t(f["x"]), taps), _t(f["y_f32"]))
+        assert torch.equal(triton_causal_fir(_t(f["x_bf16"]), taps).view(torch.int16),
+                           _t(f["y_bf16"]).view(torch.int16))
