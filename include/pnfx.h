@@ -4,7 +4,8 @@
  * Every entry point takes device pointers, element strides and sizes, and a
  * hipStream_t passed as `void*` (NULL = the legacy default stream).  Kernels are
  * enqueued on that stream; nothing blocks the host and nothing is allocated:
- * callers own every buffer, including the workspace of pnfx_flash_bwd.
+ * callers own every buffer, including the workspace of pnfx_flash_bwd (the one
+ * exception, pnfx_flash_bwd_noalloc, uses a scratch array the library holds).
  *
  * Return value: PNFX_OK (0) or a negative PNFX_E* code; pnfx_last_error()
  * returns a thread-local message for the last failing call on that thread.
@@ -181,6 +182,30 @@ int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int64_t qsh, i
                           int64_t workspace_bytes, int64_t B, int64_t H, int64_t N, int64_t D,
                           const float* tau, float scale, float gamma, int has_gamma, int causal,
                           int dtype, void* stream);
+
+/*
+ * pnfx_flash_bwd without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments and results as
+ * pnfx_flash_bwd (bitwise the same outputs); the workspace is a scratch array of
+ * PNFX_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on until the
+ * process ends.  Shapes whose pnfx_flash_bwd_workspace_size exceeds that return PNFX_EINVAL
+ * (C4, B=4 H=16 N=8192 D=64, needs 151 MB and fits).  Allocates nothing: the first call on
+ * a device looks up the array's address there (the current device must be the stream's).
+ * Calls that overlap on one GPU (different streams, or threads) share the array and race.
+ */
+#define PNFX_NOALLOC_SCRATCH_BYTES (160ll << 20)
+int pnfx_flash_bwd_noalloc(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
+                           int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
+                           int64_t vsh, int64_t vsn, const void* o, int64_t osb, int64_t osh,
+                           int64_t osn, const void* o_lo, const void* dout, int64_t dosb,
+                           int64_t dosh, int64_t dosn, const float* M, const float* Z,
+                           const uint8_t* tile_mask, void* dq, int64_t dqsb, int64_t dqsh,
+                           int64_t dqsn, void* dk, int64_t dksb, int64_t dksh, int64_t dksn,
+                           void* dv, int64_t dvsb, int64_t dvsh, int64_t dvsn, float* dtau,
+                           int64_t B, int64_t H, int64_t N, int64_t D, const float* tau,
+                           float scale, float gamma, int has_gamma, int causal, int dtype,
+                           void* stream);
 
 #ifdef __cplusplus
 }

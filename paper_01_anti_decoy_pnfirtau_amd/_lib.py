@@ -15,6 +15,7 @@ ABI_VERSION = 3
 PNFX_F32 = 0
 PNFX_BF16 = 1
 PNFX_BWD_PREPARE, PNFX_BWD_DKDV, PNFX_BWD_DQ, PNFX_BWD_ALL = 1, 2, 4, 7
+PNFX_NOALLOC_SCRATCH_BYTES = 160 << 20
 
 _lib = None
 
@@ -50,6 +51,8 @@ def _declare(lib: ctypes.CDLL) -> None:
             + [vp, vp, i64, i64, i64, i64, i64, vp, f32, f32, i32, i32, i32, vp], i32),
     }
     sig["pnfx_flash_bwd_stages"] = ([i32] + sig["pnfx_flash_bwd"][0], i32)
+    bwd = sig["pnfx_flash_bwd"][0]  # pnfx_flash_bwd without (workspace, workspace_bytes)
+    sig["pnfx_flash_bwd_noalloc"] = (bwd[:37] + bwd[39:], i32)
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
         fn.argtypes = args
@@ -84,4 +87,5 @@ def exported_symbols() -> list[str]:
         "pnfx_abi_version", "pnfx_last_error", "pnfx_fir_fwd", "pnfx_fir_bwd",
         "pnfx_pn_rows_fwd", "pnfx_pn_rows_bwd", "pnfx_flash_fwd", "pnfx_flash_fwd_workspace_size",
         "pnfx_flash_bwd_workspace_size", "pnfx_flash_bwd", "pnfx_flash_bwd_stages",
+        "pnfx_flash_bwd_noalloc",
     ]

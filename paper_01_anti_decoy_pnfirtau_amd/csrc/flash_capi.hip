@@ -1,5 +1,14 @@
 // C-ABI entry points of the flash path: argument checks, workspace carving, dtype dispatch.
+#include <mutex>
+
 #include "flash.h"
+
+// Scratch memory of pnfx_flash_bwd_noalloc: the backward's workspace for callers that cannot
+// allocate.  Each GPU the library runs on holds its own copy until the process ends.  In
+// host code `scratch` names a host-side stand-in, not device memory: its device address is
+// taken once per device with hipGetSymbolAddress (scratch_address below) and only that
+// address is handed to kernels.
+static __device__ __align__(256) uint8_t scratch[PNFX_NOALLOC_SCRATCH_BYTES];
 
 namespace pnfx {
 namespace {
@@ -26,6 +35,45 @@ int check_shape(int64_t B, int64_t H, int64_t N, int64_t D) {
                (long long)D);
   PNFX_REQUIRE(B * H <= (1ll << 30) && N <= (1ll << 28) && B * H * ((N + 127) / 128) < (1ll << 31),
                "flash: shape too large for the launch grid");
+  return PNFX_OK;
+}
+
+// Device address of `scratch` on the current device, taken on the first call on that device
+// (with it current) and kept per device.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+int scratch_address(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("flash_bwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return PNFX_ELAUNCH;
+  }
+  PNFX_REQUIRE(dev >= 0 && dev < kMaxDevices, "flash_bwd_noalloc: device %d out of range", dev);
+  if (stream) {
+    int sdev = -1;
+    e = hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) {
+      set_error("flash_bwd_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+      return PNFX_ELAUNCH;
+    }
+    PNFX_REQUIRE(sdev == dev, "flash_bwd_noalloc: the stream is on device %d, device %d is current",
+                 sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("flash_bwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                hipGetErrorString(e));
+      return PNFX_ELAUNCH;
+    }
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
   return PNFX_OK;
 }
 
@@ -141,5 +189,37 @@ extern "C" int pnfx_flash_bwd(const void* q, int64_t qsb, int64_t qsh, int64_t q
                                o, osb, osh, osn, o_lo, dout, dosb, dosh, dosn, M, Z,
                                tile_mask, dq, dqsb, dqsh, dqsn, dk, dksb, dksh, dksn, dv, dvsb,
                                dvsh, dvsn, dtau, workspace, workspace_bytes, B, H, N, D, tau,
+                               scale, gamma, has_gamma, causal, dtype, stream);
+}
+
+extern "C" int pnfx_flash_bwd_noalloc(const void* q, int64_t qsb, int64_t qsh, int64_t qsn,
+                                      const void* k, int64_t ksb, int64_t ksh, int64_t ksn,
+                                      const void* v, int64_t vsb, int64_t vsh, int64_t vsn,
+                                      const void* o, int64_t osb, int64_t osh, int64_t osn,
+                                      const void* o_lo, const void* dout, int64_t dosb,
+                                      int64_t dosh, int64_t dosn, const float* M, const float* Z,
+                                      const uint8_t* tile_mask, void* dq, int64_t dqsb,
+                                      int64_t dqsh, int64_t dqsn, void* dk, int64_t dksb,
+                                      int64_t dksh, int64_t dksn, void* dv, int64_t dvsb,
+                                      int64_t dvsh, int64_t dvsn, float* dtau, int64_t B,
+                                      int64_t H, int64_t N, int64_t D, const float* tau,
+                                      float scale, float gamma, int has_gamma, int causal,
+                                      int dtype, void* stream) {
+  int rc;
+  if ((rc = check_shape(B, H, N, D))) return rc;
+  const int64_t need = pnfx_flash_bwd_workspace_size(B, H, N, D);
+  PNFX_REQUIRE(need <= (int64_t)PNFX_NOALLOC_SCRATCH_BYTES,
+               "flash_bwd_noalloc: B=%lld H=%lld N=%lld D=%lld needs %lld bytes of scratch, "
+               "more than the %lld the library holds (use pnfx_flash_bwd with a workspace)",
+               (long long)B, (long long)H, (long long)N, (long long)D, (long long)need,
+               (long long)PNFX_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((rc = scratch_address(stream, &ws))) return rc;
+  // Nothing in the scratch needs clearing: every byte the kernels read is written earlier in
+  // the same call (the key-tile activity bytes are zeroed by the prepare kernel).
+  return pnfx_flash_bwd_stages(PNFX_BWD_ALL, q, qsb, qsh, qsn, k, ksb, ksh, ksn, v, vsb, vsh, vsn,
+                               o, osb, osh, osn, o_lo, dout, dosb, dosh, dosn, M, Z, tile_mask,
+                               dq, dqsb, dqsh, dqsn, dk, dksb, dksh, dksn, dv, dvsb, dvsh, dvsn,
+                               dtau, ws, (int64_t)PNFX_NOALLOC_SCRATCH_BYTES, B, H, N, D, tau,
                                scale, gamma, has_gamma, causal, dtype, stream);
 }

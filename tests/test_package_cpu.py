@@ -138,6 +138,11 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert rc == -1 and b"K=17" in lib.pnfx_last_error()
     need = lib.pnfx_flash_bwd_workspace_size(4, 16, 8192, 64)
     assert need >= 4 * 16 * 8192 * 32
+    # the no-allocation backward refuses a shape past its scratch before any device call
+    rc = lib.pnfx_flash_bwd_noalloc(*([None, 0, 0, 0] * 4), None, None, 0, 0, 0, None, None, None,
+                                    *([None, 0, 0, 0] * 3), None, 4, 16, 16384, 64, None, 0.125,
+                                    0.5, 1, 1, 1, None)
+    assert rc == -1 and b"scratch" in lib.pnfx_last_error()
 
 
 def test_hip_ops_refuse_cpu_tensors():
