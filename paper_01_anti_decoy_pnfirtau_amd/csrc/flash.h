@@ -33,6 +33,8 @@ struct BwdParams {
   double* partials;  // tau partials, one per wave of the dq kernel (bf16: [B*H][N/128][4])
   void *qx, *dox;    // bf16, D <= 64: Q and dO rows scaled by g/Z, contiguous [B*H, N, D]
   uint8_t* ktact;    // [B*H][nk64]: 64-key tiles with any active tile-mask entry (mask given)
+  uint8_t* amap;     // [B*H][nq32][nk64] (mask given, N <= kAmapMaxN): bit 0 the sub-tile's
+                     // activity, bit 1 + h a peak tie in its 32-key half h (dQ -> dK/dV)
   float* dtau;
   int B, H, N, nq32, nk64, nkvb;
   const float* tau;
@@ -46,18 +48,22 @@ inline int bwd_nkvb(int64_t N, int64_t D) {
 }
 // Workspace of the backward: row constants, tau partials (fp64, one per 32 query rows: the
 // bf16 dq kernel's waves; the fp32 kernels use one per 64 rows), and for D <= 64 the
-// row-scaled copies of Q and dO that the bf16 dK/dV kernel reads, and one activity byte per
-// 64-key tile.
+// row-scaled copies of Q and dO that the bf16 dK/dV kernel reads, one activity byte per
+// 64-key tile, and the activity/tie map of the 32-query x 64-key sub-tiles.
+// The activity/tie map of the backward (BwdParams::amap) is kept up to this sequence length:
+// N^2/2048 bytes per (b, h), 2 MiB at N = 65536.
+constexpr int64_t kAmapMaxN = 65536;
 struct BwdWorkspace {
-  int64_t rc_bytes, parts_bytes, xt_bytes, kt_bytes;
+  int64_t rc_bytes, parts_bytes, xt_bytes, kt_bytes, amap_bytes;
   BwdWorkspace(int64_t B, int64_t H, int64_t N, int64_t D) {
     const int64_t slots = B * H * ((N + 127) / 128) * 4;
     rc_bytes = round256(B * H * N * 8 * 4);
     parts_bytes = round256(slots * 8);
     xt_bytes = D <= 64 ? round256(B * H * N * D * 2) : 0;  // each of Qx, dOx
     kt_bytes = round256(B * H * ((N + 63) / 64));
+    amap_bytes = N <= kAmapMaxN ? round256(B * H * ((N + 31) / 32) * ((N + 63) / 64)) : 0;
   }
-  int64_t total() const { return rc_bytes + parts_bytes + 2 * xt_bytes + kt_bytes; }
+  int64_t total() const { return rc_bytes + parts_bytes + 2 * xt_bytes + kt_bytes + amap_bytes; }
   static int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
 };
 

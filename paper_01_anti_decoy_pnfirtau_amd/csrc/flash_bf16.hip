@@ -722,6 +722,43 @@ __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2],
       }
 }
 
+// ds_kq without the peak-tie term, for half tiles where no row of the wave has a key at its
+// peak: dS/(10 scale x) = u^9 (dW - D).
+__device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2]) {
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float u = relu_mfma(s[kk][qb][i]);
+        const float u2 = u * u;
+        const float u4 = u2 * u2;
+        dw[kk][qb][i] = (u4 * u4 * u) * dw[kk][qb][i];
+      }
+}
+
+// Whether some lane of the wave holds a score tied at its row's peak M on a row whose tie
+// term is non-zero.  Every score is <= M (M is the forward's maximum of the same MFMA
+// values), so a tie is a lane maximum equal to M; the maximum is an integer max over the raw
+// bit patterns (order-preserving for positive floats; negatives, and the mask's -1, stay
+// below any M > 0).  Half a VALU op per score against three for the tie compare, select and
+// count of ds_kq.
+__device__ __forceinline__ bool any_peak_tie(const f32x4 (&s)[2][2], const float (&rM)[2],
+                                             const float (&rG)[2]) {
+  bool t = false;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    int mx = f2i(s[0][qb][0]);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = max(mx, f2i(s[kk][qb][i]));
+    t = t || (mx >= f2i(rM[qb]) && rG[qb] != 0.f);
+  }
+  return __any(t);
+}
+
 // dQ: query-parallel, same tiling as the forward (4 waves x 32 rows, 64-key tiles), K and V
 // tiles software-pipelined through LDS (double-buffered when it fits).
 //
@@ -817,6 +854,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
   const int ntiles = (kv_end + BN - 1) / BN;
   const uint8_t* mrow =
       (p.mask && has_rows) ? p.mask + ((int64_t)bh * p.nq32 + (qrow0 >> 5)) * p.nk64 : nullptr;
+  // Activity/tie byte of each (32-row group, 64-key tile) for the dK/dV kernel.
+  uint8_t* arow = (p.amap && has_rows) ? p.amap + ((int64_t)bh * p.nq32 + (qrow0 >> 5)) * p.nk64
+                                       : nullptr;
   // The activity byte of the next tile is fetched one iteration ahead and kept as a raw
   // byte until it is tested, so that its wait does not also wait for the tile prefetch.
   int act_next;
@@ -836,7 +876,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
     const int act = act_next;
     if (mrow && pre) act_next = mrow[t + 1];
     const bool work = has_rows && !(CAUSAL && n0 > qrow0 + 31) && act != 0;
+    int code = 0;  // the activity/tie byte of this (32-row group, tile)
     if (work) {
+      code = 1;
       // key tile t has an active entry: the dK/dV kernel schedules it among the active tiles
       if (mrow && lane == 0) p.ktact[(int64_t)bh * p.nk64 + t] = 1;
       const bf16* Kc = bc.k;
@@ -869,7 +911,12 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
         }
         affine_kq<PS>(s, scale, ntau);
         if (masked) mask_kq(s, n0, hf, qrow0, N, CAUSAL, g, r16);
-        ds_kq<true>(s, dw, cnt, rM, rG);
+        if (any_peak_tie(s, rM, rG)) {
+          ds_kq<true>(s, dw, cnt, rM, rG);
+          code |= 2 << hf;
+        } else {
+          ds_kq_notie(s, dw);
+        }
         bf16x8 pf[2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -885,6 +932,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
         adt[1] = mfma16x16x32(ones, pf[1], adt[1]);
       }
     }
+    if (arow && lane == 0) arow[t] = (uint8_t)code;
   };
   for (int pass = 0;; ++pass) {
   act_next = mrow ? mrow[0] : 1;
@@ -1040,6 +1088,47 @@ __device__ __forceinline__ void w_ds_qk_x(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB],
   }
 }
 
+// w_ds_qk_x without the peak-tie term (no row of the half has a key of this wave at its peak).
+template <int KB>
+__device__ __forceinline__ void w_ds_qk_x_notie(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB]) {
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const float u = relu_mfma(s[qq][kb][i]);
+        const float u2 = u * u;
+        const float u4 = u2 * u2;
+        const float u9 = u4 * u4 * u;
+        s[qq][kb][i] = u9 * u;
+        dw[qq][kb][i] = u9 * dw[qq][kb][i];
+      }
+}
+
+// w_ds_qk without the peak-tie term.
+template <int KB>
+__device__ __forceinline__ void w_ds_qk_notie(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB],
+                                              const float* rc, int pitch, int r4) {
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq) {
+    f32x4 c[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) c[k] = *reinterpret_cast<const f32x4*>(rc + (k + 1) * pitch + r4 + 4 * qq);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const float a = relu_mfma(s[qq][kb][i]) * c[0][i];
+        const float a2 = a * a;
+        const float a4 = a2 * a2;
+        const float a9 = a4 * a4 * a;
+        s[qq][kb][i] = a9 * a;
+        dw[qq][kb][i] = a9 * __builtin_fmaf(c[1][i], dw[qq][kb][i], c[2][i]);
+      }
+  }
+}
+
 // Position e of the key-tile order of one (b, h): the tiles with act[t] != 0 ascending, then
 // the others ascending.  Returns the tile (or -1 past the end) and whether it is active.
 // Wave-uniform; two sweeps of nk64 bytes with ballots.
@@ -1170,7 +1259,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   // first query tile: the causal diagonal of the workgroup's lowest active tile (the first
   // in the order); none if the workgroup has only silent tiles
   const int qt0 = !wg_active ? nqt : (CAUSAL ? tile0 * 64 / BMQ : 0);
-  const uint8_t* mcol = (p.mask && live) ? p.mask + (int64_t)bh * p.nq32 * p.nk64 + wtile : nullptr;
+  // Per-sub-tile activity, from the dQ stage's activity/tie map (bit 0 active, bit 1 + h a
+  // peak tie in 32-key half h) or else from the forward's tile mask (no tie information: the
+  // tie test runs everywhere).
+  const uint8_t* msrc = p.amap ? p.amap : p.mask;
+  const uint8_t* mcol = (msrc && live) ? msrc + (int64_t)bh * p.nq32 * p.nk64 + wtile : nullptr;
+  const int tie_bit = p.amap ? 2 << (((KPW * w) % 64) / 32) : 0xff;
 
   // Tiles go straight from global memory to LDS buffer bb; rows >= N repeat row N - 1 (their
   // scores are masked), including their row constants.
@@ -1192,7 +1286,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   // Activity of a 64-row query tile for this wave's keys: either of its two 32-row halves.
   // Fetched one iteration ahead and kept as raw bytes until tested, so that its wait does
   // not also wait for the tile prefetch.
-  int act_next[2] = {1, 0};
+  int act_next[2] = {0xff, 0xff};  // without a map: every half active, tie test everywhere
   auto fetch_active = [&](int m) {
     const int r32 = m >> 5;
     act_next[0] = mcol[(int64_t)r32 * p.nk64];
@@ -1208,7 +1302,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     if (pre) load_tile(m0 + BMQ, bn);
     const int act0 = act_next[0], act1 = act_next[1];
     if (mcol && pre) fetch_active(m0 + BMQ);
-    const bool work = live && !(CAUSAL && m0 + BMQ - 1 < kw0) && (act0 | act1) != 0;
+    const bool work = live && !(CAUSAL && m0 + BMQ - 1 < kw0) && ((act0 | act1) & 1) != 0;
     if (work) {
       const bf16* Qc = bc.q;
       const bf16* dOc = bc.o;
@@ -1218,6 +1312,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         if (CAUSAL && m0 + 32 * hf + 31 < kw0) continue;  // rows of this half precede the keys
+        // wave-uniform (one byte, loaded by every lane): keep it in a scalar register
+        const int code = __builtin_amdgcn_readfirstlane(hf ? act1 : act0);
+        if (!(code & 1)) continue;          // a silent 32-row half
+        const bool ties = (code & tie_bit) != 0;
         f32x4 s[2][KB], dw[2][KB];
 #pragma unroll
         for (int qq = 0; qq < 2; ++qq) {
@@ -1246,8 +1344,13 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         affine_qk<KB, PS>(s, scale, ntau);
         if (masked) mask_qk<KB>(s, m0, hf, kw0, N, CAUSAL, g, r16);
         // rows 32 hf + 8 g + 4 qq + (0..3) of the tile are perm_row(2 hf + qq, 4 g + i)
-        if constexpr (XT) w_ds_qk_x<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
-        else w_ds_qk<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
+        if constexpr (XT) {
+          if (ties) w_ds_qk_x<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
+          else w_ds_qk_x_notie<KB>(s, dw);
+        } else {
+          if (ties) w_ds_qk<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
+          else w_ds_qk_notie<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
+        }
         bf16x8 wf[KB], sf[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
