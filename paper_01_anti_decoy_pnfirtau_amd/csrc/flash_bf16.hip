@@ -384,6 +384,9 @@ __device__ __forceinline__ float max_nonneg(float a, float b) {
   return __builtin_bit_cast(float, max(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b)));
 }
 
+// Longest compacted key-tile list of the forward kernel (N <= 65536).
+constexpr int kMaxListTiles = 1024;
+
 // COUNT: also count the peak ties (Nmax); the training path leaves that to the backward.
 template <int D, bool CAUSAL, bool PS, bool COUNT>
 __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdParams p) {
@@ -489,9 +492,37 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
     qb_w = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, qb_w)));
     qb_wg = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, qb_wg)));
   }
-  // wave-uniform: kept in scalar registers
-  float kn_cur = bound ? i2f(__builtin_amdgcn_readfirstlane(f2i(kn[0]))) : 0.f;  // tile t
-  float kn_next = (bound && ntiles > 1) ? i2f(__builtin_amdgcn_readfirstlane(f2i(kn[1]))) : 0.f;
+  // With the bound, the key loop runs over the tiles the workgroup cannot bound silent only,
+  // compacted into a list (no load, barrier or mask lookup for the others); the mask bytes of
+  // the skipped tiles are written here, the loop writes the rest.
+  __shared__ uint16_t tl_s[BOUND ? kMaxListTiles : 1];
+  int nlist = ntiles;
+  if (bound) {
+    // every wave forms the ballots (and zeroes its own skipped mask bytes); wave 0 writes the
+    // list
+    int base = 0;
+    for (int c = 0; c < p.nk64; c += 64) {
+      const int t = c + lane;
+      const bool f = t < ntiles && !(qb_wg * kn[t] <= tau);
+      if (!f && mrow && t < p.nk64) mrow[t] = 0;
+      const uint64_t bal = __ballot(f);
+      if (w == 0 && f) tl_s[base + __popcll(bal & ((1ull << lane) - 1ull))] = (uint16_t)t;
+      base += __popcll(bal);
+    }
+    nlist = base;
+    __syncthreads();
+  } else if (mrow) {
+    for (int t = ntiles + lane; t < p.nk64; t += 64) mrow[t] = 0;
+  }
+  const bool ident = nlist == ntiles;  // nothing skipped: the list is 0, 1, 2, ...
+  // (read into a scalar register: tile addresses stay scalar bases for the tile loads)
+  const auto tile_at = [&](int e) {
+    return ident ? e : __builtin_amdgcn_readfirstlane((int)tl_s[e]);
+  };
+  // The list entries are read one step ahead (t_cur, t_nxt), off the prefetch's path;
+  // wave-uniform values are kept in scalar registers.
+  int t_cur = nlist > 0 ? tile_at(0) : 0, t_nxt = nlist > 1 ? tile_at(1) : 0;
+  float kn_cur = (bound && nlist > 0) ? i2f(__builtin_amdgcn_readfirstlane(f2i(kn[t_cur]))) : 0.f;
 
   // Software pipeline: tile t+1 streams from HBM/L2 straight into one LDS buffer while tile
   // t is computed from the other; one barrier per tile.
@@ -500,16 +531,18 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
     kdma.load(K, p.ksn, n, N, bb.k, w);
     vdma.load(V, p.vsn, n, N, bb.v, w);
   };
-  auto step = [&](int t, const KVBuf& bc, const KVBuf& bn) {
+  // Entry e of the list: tile t = t_cur, computed from buffer bc while t_nxt streams into
+  // buffer bn.
+  auto step = [&](int e, const KVBuf& bc, const KVBuf& bn) {
+    const int t = t_cur;
     const int n0 = t * BN;
     wait_vmem();  // this wave's part of tile t is in LDS
     __syncthreads();
-    const bool pre = t + 1 < ntiles;
-    if (pre && !(bound && qb_wg * kn_next <= tau)) load_tile(n0 + BN, bn);
-    const bool bounded = bound && qb_w * kn_cur <= tau;  // implied for every unloaded tile
-    kn_cur = kn_next;
-    if (bound && t + 2 < ntiles)
-      kn_next = i2f(__builtin_amdgcn_readfirstlane(f2i(kn[t + 2])));
+    if (e + 1 < nlist) load_tile(t_nxt * BN, bn);
+    const bool bounded = bound && qb_w * kn_cur <= tau;  // the wave's own bound
+    if (bound && e + 1 < nlist) kn_cur = i2f(__builtin_amdgcn_readfirstlane(f2i(kn[t_nxt])));
+    t_cur = t_nxt;
+    if (e + 2 < nlist) t_nxt = tile_at(e + 2);
     bool active = false;
     if (has_rows && !bounded && !(CAUSAL && n0 > qrow0 + 31)) {
       const bf16* Kc = bc.k;
@@ -576,13 +609,11 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
     }
     if (mrow && lane == 0) mrow[t] = active ? 1 : 0;
   };
-  load_tile(0, buf0);
-  for (int t = 0; t < ntiles; t += 2) {
-    step(t, buf0, buf1);
-    if (t + 1 < ntiles) step(t + 1, buf1, buf0);
+  if (nlist > 0) load_tile(t_cur * BN, buf0);
+  for (int e = 0; e < nlist; e += 2) {
+    step(e, buf0, buf1);
+    if (e + 1 < nlist) step(e + 1, buf1, buf0);
   }
-  if (mrow && lane == 0)
-    for (int t = ntiles; t < p.nk64; ++t) mrow[t] = 0;
 
   // Epilogue: reduce the lane-local statistics over the four lane groups of a row.
   bf16* O = static_cast<bf16*>(p.o) + b * p.osb + h * p.osh;
