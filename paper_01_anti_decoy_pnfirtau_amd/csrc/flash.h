@@ -30,7 +30,7 @@ struct BwdParams {
   const float* Z;
   const uint8_t* mask;
   float* rc;         // row constants [B*H*N][8], layout private to each dtype's kernels
-  double* partials;  // tau partials, one per wave of the dq kernel (bf16: [B*H][N/128][4])
+  double* partials;  // tau partials, one per wave of the dq kernel (bf16: [B*H][N/BM][4])
   void *qx, *dox;    // bf16, D <= 64: Q and dO rows scaled by g/Z, contiguous [B*H, N, D]
   uint8_t* ktact;    // [B*H][nk64]: 64-key tiles with any active tile-mask entry (mask given)
   uint8_t* amap;     // [B*H][nq32][nk64] (mask given, N <= kAmapMaxN): bit 0 the sub-tile's
@@ -41,13 +41,18 @@ struct BwdParams {
   float scale, gamma;
 };
 
+// 16-row MFMA query blocks per wave of the bf16 dQ kernel (workgroups of four waves cover
+// 64 * dq_qblocks(D) query rows).
+constexpr int dq_qblocks(int64_t D) { return D <= 64 ? 2 : 1; }
+inline int64_t dq_rows_per_wg(int64_t D) { return 64 * dq_qblocks(D); }
+
 // Key blocks of the key-parallel backward kernel.
 inline int bwd_nkvb(int64_t N, int64_t D) {
   const int64_t bnk = D <= 64 ? 128 : 64;
   return (int)((N + bnk - 1) / bnk);
 }
-// Workspace of the backward: row constants, tau partials (fp64, one per 32 query rows: the
-// bf16 dq kernel's waves; the fp32 kernels use one per 64 rows), and for D <= 64 the
+// Workspace of the backward: row constants, tau partials (fp64, one per wave of the bf16 dq
+// kernel, four per workgroup; the fp32 kernels use one per 64 rows), and for D <= 64 the
 // row-scaled copies of Q and dO that the bf16 dK/dV kernel reads, one activity byte per
 // 64-key tile, and the activity/tie map of the 32-query x 64-key sub-tiles.
 // The activity/tie map of the backward (BwdParams::amap) is kept up to this sequence length:
@@ -56,7 +61,8 @@ constexpr int64_t kAmapMaxN = 65536;
 struct BwdWorkspace {
   int64_t rc_bytes, parts_bytes, xt_bytes, kt_bytes, amap_bytes;
   BwdWorkspace(int64_t B, int64_t H, int64_t N, int64_t D) {
-    const int64_t slots = B * H * ((N + 127) / 128) * 4;
+    const int64_t rw = dq_rows_per_wg(D);
+    const int64_t slots = B * H * ((N + rw - 1) / rw) * 4;
     rc_bytes = round256(B * H * N * 8 * 4);
     parts_bytes = round256(slots * 8);
     xt_bytes = D <= 64 ? round256(B * H * N * D * 2) : 0;  // each of Qx, dOx

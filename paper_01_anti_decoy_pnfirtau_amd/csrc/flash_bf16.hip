@@ -251,11 +251,11 @@ __device__ __forceinline__ void map_block(int nblk, int BH, bool heavy_last_inde
 // Scores in the key-major layout S^T (register i of lane group g holds key
 // perm_row(blk, 4g+i), lane r16 holds query 16qb+r16).  Without the scale fold, the scores
 // are first mapped to s*scale - tau (PS: the MFMA already produced that).
-template <bool PS>
-__device__ __forceinline__ void affine_kq(f32x4 (&s)[2][2], float scale, float ntau) {
+template <bool PS, int QB>
+__device__ __forceinline__ void affine_kq(f32x4 (&s)[2][QB], float scale, float ntau) {
   if (PS) return;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -265,10 +265,11 @@ __device__ __forceinline__ void affine_kq(f32x4 (&s)[2][2], float scale, float n
 // Causal and sequence-end mask, in place: entries outside it become -1, which the rectifier
 // maps to 0.  Only tiles that straddle the diagonal or the sequence end run it, so the
 // common tile's score code has no mask operations and no second copy.
-__device__ __forceinline__ void mask_kq(f32x4 (&s)[2][2], int n0, int hf, int qrow0, int N,
+template <int QB>
+__device__ __forceinline__ void mask_kq(f32x4 (&s)[2][QB], int n0, int hf, int qrow0, int N,
                                         bool causal, int g, int r16) {
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -734,11 +735,11 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
 // dS/(10 scale x) for the 16 scores a lane holds in one 32-key half tile of the dQ kernel
 // (S^T layout, one query row per lane), written over dw = dW - D: u^9 dw + [u == M] G''.
 // COUNT also counts the peak ties per query block.
-template <bool COUNT>
-__device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2], int (&cnt)[2],
-                                      const float (&rM)[2], const float (&rG)[2]) {
+template <bool COUNT, int QB>
+__device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB], int (&cnt)[QB],
+                                      const float (&rM)[QB], const float (&rG)[QB]) {
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -755,9 +756,10 @@ __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2],
 
 // ds_kq without the peak-tie term, for half tiles where no row of the wave has a key at its
 // peak: dS/(10 scale x) = u^9 (dW - D).
-__device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][2], f32x4 (&dw)[2][2]) {
+template <int QB>
+__device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB]) {
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -775,11 +777,12 @@ __device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][2], f32x4 (&dw)[
 // bit patterns (order-preserving for positive floats; negatives, and the mask's -1, stay
 // below any M > 0).  Half a VALU op per score against three for the tie compare, select and
 // count of ds_kq.
-__device__ __forceinline__ bool any_peak_tie(const f32x4 (&s)[2][2], const float (&rM)[2],
-                                             const float (&rG)[2]) {
+template <int QB>
+__device__ __forceinline__ bool any_peak_tie(const f32x4 (&s)[2][QB], const float (&rM)[QB],
+                                             const float (&rG)[QB]) {
   bool t = false;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     int mx = f2i(s[0][qb][0]);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
@@ -799,13 +802,16 @@ __device__ __forceinline__ bool any_peak_tie(const f32x4 (&s)[2][2], const float
 // row constants (for the dK/dV kernel) and the tau partial is corrected to G per row.  A row
 // with two or more ties got too much tie gradient in dQ: if the workgroup has any such row
 // (rare: duplicated keys), it runs the key loop a second time with G/Nmax.
-// At D = 128 the dQ accumulators and the Q/dO fragments need more than the 256 registers a
-// wave has at two workgroups per CU: one workgroup per CU gives each wave 512 (VGPRs plus
-// AGPRs) and no spills, which is far faster than spilling.
+// At D = 128 the dQ accumulators and the Q/dO fragments of 32 rows need more than the 256
+// registers a wave has at two workgroups per CU, so each wave takes 16 rows there (64-row
+// workgroups, two per CU) instead of running one 128-row workgroup per CU.
 template <int D, bool CAUSAL, bool PS>
-__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdParams p) {
+__global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   constexpr bool XT = D <= 64;  // writes the row-scaled Q and dO of the dK/dV kernel
-  constexpr int BM = 128, BN = 64;
+  // Query rows per wave: 32 (two 16-row MFMA blocks) up to D = 64; 16 at D = 128, where the
+  // dQ accumulators and the Q/dO fragments of 32 rows would not fit two workgroups per CU.
+  constexpr int QB = dq_qblocks(D), RPW = 16 * QB;
+  constexpr int BM = 4 * RPW, BN = 64;
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
@@ -829,21 +835,21 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
   const bf16* V = static_cast<const bf16*>(p.v) + b * p.vsb + h * p.vsh;
   const bf16* dO = static_cast<const bf16*>(p.dout) + b * p.dosb + h * p.dosh;
   const int m0 = qblk * BM;
-  const int qrow0 = m0 + 32 * w;
+  const int qrow0 = m0 + RPW * w;
   const bool has_rows = qrow0 < N;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
   const float ds_mult = 10.f * scale;  // the score loops form dS/(10 scale x)
   const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
 
-  bf16x8 qf[2][KS], dof[2][KS];
-  float rM[2], rG[2], rX[2];
-  f32x4 dw_init[2];  // -D: the dW accumulator starts there
+  bf16x8 qf[QB][KS], dof[QB][KS];
+  float rM[QB], rG[QB], rX[QB];
+  f32x4 dw_init[QB];  // -D: the dW accumulator starts there
   // D <= 64: the rows of Q and dO scaled by x = g/Z, for the dK/dV kernel (which runs next).
   bf16* Qx = XT ? static_cast<bf16*>(p.qx) + (int64_t)bh * N * D : nullptr;
   bf16* dOx = XT ? static_cast<bf16*>(p.dox) + (int64_t)bh * N * D : nullptr;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const int row = qrow0 + 16 * qb + r16;
     const bool rok = row < N;
     rM[qb] = rok ? rc_plane(p, bh, 0)[row] : 0.f;
@@ -866,28 +872,32 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
   }
 
   const f32x4 s_init = PS ? f32x4{ntau, ntau, ntau, ntau} : f32x4{0.f, 0.f, 0.f, 0.f};
-  int cnt[2] = {0, 0};  // lane-local tie counts (first pass)
+  int cnt[QB] = {};  // lane-local tie counts (first pass)
   // Sum of every ds the wave forms, accumulated by the MFMA: a constant A fragment whose
   // row 0 is all ones turns the ds^T operand into its column sums (lanes g == 0, slot 0).
-  f32x4 adt[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  f32x4 adt[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) adt[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
   bf16x8 ones = zero_bf16x8();
   if (r16 == 0) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) ones[e] = (bf16)1.0f;
   }
-  f32x4 acc[DB][2];
+  f32x4 acc[DB][QB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) acc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int qb = 0; qb < QB; ++qb) acc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int kv_end = CAUSAL ? min(m0 + BM, N) : N;
   const int ntiles = (kv_end + BN - 1) / BN;
   const uint8_t* mrow =
       (p.mask && has_rows) ? p.mask + ((int64_t)bh * p.nq32 + (qrow0 >> 5)) * p.nk64 : nullptr;
-  // Activity/tie byte of each (32-row group, 64-key tile) for the dK/dV kernel.
-  uint8_t* arow = (p.amap && has_rows) ? p.amap + ((int64_t)bh * p.nq32 + (qrow0 >> 5)) * p.nk64
-                                       : nullptr;
+  // Activity/tie byte of each (32-row group, 64-key tile) for the dK/dV kernel (one wave
+  // per group: at 16 rows per wave the launcher passes no map).
+  uint8_t* arow = (p.amap && has_rows && QB == 2)
+                      ? p.amap + ((int64_t)bh * p.nq32 + (qrow0 >> 5)) * p.nk64
+                      : nullptr;
   // The activity byte of the next tile is fetched one iteration ahead and kept as a raw
   // byte until it is tested, so that its wait does not also wait for the tile prefetch.
   int act_next;
@@ -906,7 +916,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
     if (pre) load_tile(n0 + BN, bn);
     const int act = act_next;
     if (mrow && pre) act_next = mrow[t + 1];
-    const bool work = has_rows && !(CAUSAL && n0 > qrow0 + 31) && act != 0;
+    const bool work = has_rows && !(CAUSAL && n0 > qrow0 + RPW - 1) && act != 0;
     int code = 0;  // the activity/tie byte of this (32-row group, tile)
     if (work) {
       code = 1;
@@ -917,8 +927,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
       const bool masked = (CAUSAL && n0 + BN - 1 > qrow0) || n0 + BN > N;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-        if (CAUSAL && n0 + 32 * hf > qrow0 + 31) break;
-        f32x4 s[2][2], dw[2][2];
+        if (CAUSAL && n0 + 32 * hf > qrow0 + RPW - 1) break;
+        f32x4 s[2][QB], dw[2][QB];
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           bf16x8 kf[KS], vf[KS];
@@ -929,7 +939,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
             vf[ks] = ld16(Vc + off);
           }
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
+          for (int qb = 0; qb < QB; ++qb) {
             f32x4 a4 = s_init, c4 = dw_init[qb];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
@@ -948,19 +958,19 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
         } else {
           ds_kq_notie(s, dw);
         }
-        bf16x8 pf[2];
+        bf16x8 pf[QB];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
           pf[qb] = pack8(dw[0][qb][0], dw[0][qb][1], dw[0][qb][2], dw[0][qb][3], dw[1][qb][0],
                          dw[1][qb][1], dw[1][qb][2], dw[1][qb][3]);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const bf16x8 ktf = tr_frag<DK>(Kc, flt, hf, db);
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb) acc[db][qb] = mfma16x16x32(ktf, pf[qb], acc[db][qb]);
+          for (int qb = 0; qb < QB; ++qb) acc[db][qb] = mfma16x16x32(ktf, pf[qb], acc[db][qb]);
         }
-        adt[0] = mfma16x16x32(ones, pf[0], adt[0]);
-        adt[1] = mfma16x16x32(ones, pf[1], adt[1]);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) adt[qb] = mfma16x16x32(ones, pf[qb], adt[qb]);
       }
     }
     if (arow && lane == 0) arow[t] = (uint8_t)code;
@@ -979,7 +989,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
   double dsum = 0.0;
   bool multi = false;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     int c = cnt[qb];
     c += __shfl_xor(c, 16, 64);
     c += __shfl_xor(c, 32, 64);
@@ -1003,12 +1013,12 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void flash_bwd_dq_kernel(BwdP
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) acc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int qb = 0; qb < QB; ++qb) acc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   bf16* dQ = static_cast<bf16*>(p.dq) + b * p.dqsb + h * p.dqsh;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const int qrow = qrow0 + 16 * qb + r16;
     const float rowf = ds_mult * rX[qb];
     if (qrow < N) {
@@ -1493,8 +1503,11 @@ void launch_dq(const BwdParams& bp, bool causal, dim3 grid, hipStream_t st) {
 }
 
 template <int D>
-int launch_bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, hipStream_t st) {
+int launch_bwd_d(const BwdParams& bp_in, bool causal, bool has_gamma, int stages, hipStream_t st) {
   const dim3 block(256);
+  // The activity/tie map needs one dQ wave per 32-row group: not at 16 rows per wave.
+  BwdParams bp = bp_in;
+  if (dq_qblocks(D) < 2) bp.amap = nullptr;
   if (stages & PNFX_BWD_PREPARE) {
     const int64_t rows = (int64_t)bp.B * bp.H * bp.N;
     const int rpb = 256 / (D / 8);
@@ -1506,7 +1519,8 @@ int launch_bwd_d(const BwdParams& bp, bool causal, bool has_gamma, int stages, h
   }
   const bool ps = pow2_scale(bp.scale);
   if (stages & PNFX_BWD_DQ) {
-    const int nqb = (bp.N + 127) / 128;
+    const int rw = (int)dq_rows_per_wg(D);
+    const int nqb = (bp.N + rw - 1) / rw;
     const dim3 gdq((unsigned)(nqb * bp.B * bp.H));
     if (ps) launch_dq<D, true>(bp, causal, gdq, st);
     else launch_dq<D, false>(bp, causal, gdq, st);
