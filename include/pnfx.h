@@ -190,11 +190,11 @@ int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int64_t qsh, i
  * pnfx_flash_bwd (bitwise the same outputs); the workspace is a scratch array of
  * PNFX_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on until the
  * process ends.  Shapes whose pnfx_flash_bwd_workspace_size exceeds that return PNFX_EINVAL
- * (C4, B=4 H=16 N=8192 D=64, needs 151 MB and fits).  Allocates nothing: the first call on
+ * (C4, B=4 H=16 N=8192 D=64, needs 220 MB and fits).  Allocates nothing: the first call on
  * a device looks up the array's address there (the current device must be the stream's).
  * Calls that overlap on one GPU (different streams, or threads) share the array and race.
  */
-#define PNFX_NOALLOC_SCRATCH_BYTES (160ll << 20)
+#define PNFX_NOALLOC_SCRATCH_BYTES (256ll << 20)
 int pnfx_flash_bwd_noalloc(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
                            int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
                            int64_t vsh, int64_t vsn, const void* o, int64_t osb, int64_t osh,

@@ -15,7 +15,7 @@ ABI_VERSION = 3
 PNFX_F32 = 0
 PNFX_BF16 = 1
 PNFX_BWD_PREPARE, PNFX_BWD_DKDV, PNFX_BWD_DQ, PNFX_BWD_ALL = 1, 2, 4, 7
-PNFX_NOALLOC_SCRATCH_BYTES = 160 << 20
+PNFX_NOALLOC_SCRATCH_BYTES = 256 << 20
 
 _lib = None
 

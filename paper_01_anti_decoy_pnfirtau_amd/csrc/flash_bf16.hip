@@ -262,6 +262,20 @@ __device__ __forceinline__ void affine_kq(f32x4 (&s)[2][QB], float scale, float 
       for (int i = 0; i < 4; ++i) s[kk][qb][i] = __builtin_fmaf(s[kk][qb][i], scale, ntau);
 }
 
+// affine_kq with a scale and -tau per query block (the lane's row): the dQ kernel's
+// peak-normalised scores.
+template <bool PS, int QB>
+__device__ __forceinline__ void affine_kq_rows(f32x4 (&s)[2][QB], const float (&scale)[QB],
+                                               const float (&ntau)[QB]) {
+  if (PS) return;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[kk][qb][i] = __builtin_fmaf(s[kk][qb][i], scale[qb], ntau[qb]);
+}
+
 // Causal and sequence-end mask, in place: entries outside it become -1, which the rectifier
 // maps to 0.  Only tiles that straddle the diagonal or the sequence end run it, so the
 // common tile's score code has no mask operations and no second copy.
@@ -674,7 +688,16 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
 //   dS_ij = a^9 (kappa_i dW_ij - kappa_i D_i) + [u_ij == M_i] G_i/Nmax_i,
 //   G_i = D_i gate'(M_i) scale.
 // The bf16 row constants are eight planes of N floats per (b, h): M, -D, G'', x, rho, kappa,
-// -kappa D, and G/Nmax (written by the dQ kernel, which counts the ties).
+// -kappa D, and G/Nmax (written by the dQ kernel, which counts the ties).  For D <= 64 the
+// dK/dV kernel forms its scores scaled by 2^-e per row (see pow9_unit), and planes 4, 5 hold
+// M 2^-e and -tau 2^-e instead of rho and kappa; plane 7 then holds G'' 2^-9e / Nmax.
+// Exponent e of a row peak, M = m 2^e with m in [0.5, 1) (0 for silent rows), kept within
+// +-64: a peak below 2^-64 then scales to below 1 all the same, and one above 2^64 has already
+// overflowed the forward's u^10.
+__device__ __forceinline__ int peak_exponent(float M) {
+  return M > 0.f ? min(max(__builtin_amdgcn_frexp_expf(M), -64), 64) : 0;
+}
+
 __device__ __forceinline__ float* rc_plane(const BwdParams& p, int64_t bh, int k) {
   return p.rc + (bh * 8 + k) * (int64_t)p.N;
 }
@@ -726,14 +749,33 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
     rc_plane(p, bh, 1)[i] = -Dv;
     rc_plane(p, bh, 2)[i] = x > 0.f ? Dv * dgate / (10.f * x) : 0.f;
     rc_plane(p, bh, 3)[i] = x;
-    rc_plane(p, bh, 4)[i] = rho;
-    rc_plane(p, bh, 5)[i] = kappa;
+    if (D <= 64) {  // the peak-normalised scores of the dK/dV kernel
+      const int e = peak_exponent(M);
+      rc_plane(p, bh, 4)[i] = __builtin_amdgcn_ldexpf(M, -e);
+      rc_plane(p, bh, 5)[i] = __builtin_amdgcn_ldexpf(-p.tau[0], -e);
+    } else {
+      rc_plane(p, bh, 4)[i] = rho;
+      rc_plane(p, bh, 5)[i] = kappa;
+    }
     rc_plane(p, bh, 6)[i] = -kappa * Dv;
   }
 }
 
-// dS/(10 scale x) for the 16 scores a lane holds in one 32-key half tile of the dQ kernel
-// (S^T layout, one query row per lane), written over dw = dW - D: u^9 dw + [u == M] G''.
+// Rectified power chain on a peak-normalised score.  The dQ kernel forms each row's scores
+// scaled by 2^-e, where M = m 2^e (m in [0.5, 1)) is the row's peak: the scaling is exact
+// (a power of two folded into the Q fragment and the tau term), and every scaled score is
+// < 1.  So min(max(s |s|, 0), 1) -- one multiply with the clamp modifier, no separate
+// rectifier -- is exactly u^2, the chain u^4, u^8 follows, and u^9 = u^8 s (u^8 = 0 for
+// s <= 0).  Values and roundings are those of the unscaled chain times 2^-9e.
+__device__ __forceinline__ float pow9_unit(float s) {
+  const float t = __builtin_amdgcn_fmed3f(s * __builtin_fabsf(s), 0.f, 1.f);
+  const float t2 = t * t;
+  return (t2 * t2) * s;
+}
+
+// dS/(10 scale x 2^9e) for the 16 scores a lane holds in one 32-key half tile of the dQ
+// kernel (S^T layout, one query row per lane, scores scaled by 2^-e), written over
+// dw = dW - D: u^9 dw + [u == M] G'' (u, M, G'' in the scaled units).
 // COUNT also counts the peak ties per query block.
 template <bool COUNT, int QB>
 __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB], int (&cnt)[QB],
@@ -744,18 +786,15 @@ __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float u = relu_mfma(s[kk][qb][i]);
-        const float u2 = u * u;
-        const float u4 = u2 * u2;
-        const float u9 = u4 * u4 * u;
-        const bool tie = u == rM[qb];  // G'' = 0 on silent rows
+        const float u9 = pow9_unit(s[kk][qb][i]);
+        const bool tie = s[kk][qb][i] == rM[qb];  // M > 0; G'' = 0 on silent rows
         dw[kk][qb][i] = __builtin_fmaf(u9, dw[kk][qb][i], tie ? rG[qb] : 0.f);
         if (COUNT) cnt[qb] += tie ? 1 : 0;
       }
 }
 
 // ds_kq without the peak-tie term, for half tiles where no row of the wave has a key at its
-// peak: dS/(10 scale x) = u^9 (dW - D).
+// peak: dS/(10 scale x 2^9e) = u^9 (dW - D).
 template <int QB>
 __device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB]) {
 #pragma unroll
@@ -763,12 +802,7 @@ __device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][QB], f32x4 (&dw)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float u = relu_mfma(s[kk][qb][i]);
-        const float u2 = u * u;
-        const float u4 = u2 * u2;
-        dw[kk][qb][i] = (u4 * u4 * u) * dw[kk][qb][i];
-      }
+      for (int i = 0; i < 4; ++i) dw[kk][qb][i] = pow9_unit(s[kk][qb][i]) * dw[kk][qb][i];
 }
 
 // Whether some lane of the wave holds a score tied at its row's peak M on a row whose tie
@@ -843,19 +877,34 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
 
   bf16x8 qf[QB][KS], dof[QB][KS];
-  float rM[QB], rG[QB], rX[QB];
+  // Row constants.  The scores of row i are formed scaled by 2^-e_i, e_i the exponent of its
+  // peak M_i (see pow9_unit): rM and rG (the tie term) are in those units, rE holds e_i, and
+  // the row factor 10 scale x_i 2^(9 e_i) is applied to dQ and the tau partial at the end.
+  // rG0 keeps G'' unscaled for the row-constant plane of the dK/dV kernel.
+  float rM[QB], rG[QB], rG0[QB], rX[QB];
+  int rE[QB];
   f32x4 dw_init[QB];  // -D: the dW accumulator starts there
-  // D <= 64: the rows of Q and dO scaled by x = g/Z, for the dK/dV kernel (which runs next).
+  f32x4 s_init[QB];   // the score accumulator starts at -tau 2^-e (scale folded into Q)
+  float sc_e[QB], nt_e[QB];  // scale 2^-e and -tau 2^-e, for scales that are not folded
+  // D <= 64, for the dK/dV kernel (which runs next): the rows of Q scaled by 2^-e (its
+  // scores), by x 2^9e (dK) and of dO by x 2^10e (dV), x = g/Z.
   bf16* Qx = XT ? static_cast<bf16*>(p.qx) + (int64_t)bh * N * D : nullptr;
   bf16* dOx = XT ? static_cast<bf16*>(p.dox) + (int64_t)bh * N * D : nullptr;
+  bf16* Qs = XT ? static_cast<bf16*>(p.qs) + (int64_t)bh * N * D : nullptr;
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int row = qrow0 + 16 * qb + r16;
     const bool rok = row < N;
-    rM[qb] = rok ? rc_plane(p, bh, 0)[row] : 0.f;
+    const float M = rok ? rc_plane(p, bh, 0)[row] : 0.f;
     const float nxd = rok ? rc_plane(p, bh, 1)[row] : 0.f;
-    rG[qb] = rok ? rc_plane(p, bh, 2)[row] : 0.f;
+    rG0[qb] = rok ? rc_plane(p, bh, 2)[row] : 0.f;
     rX[qb] = rok ? rc_plane(p, bh, 3)[row] : 0.f;
+    rE[qb] = peak_exponent(M);
+    rM[qb] = __builtin_amdgcn_ldexpf(M, -rE[qb]);
+    rG[qb] = __builtin_amdgcn_ldexpf(rG0[qb], -9 * rE[qb]);
+    sc_e[qb] = __builtin_amdgcn_ldexpf(scale, -rE[qb]);
+    nt_e[qb] = __builtin_amdgcn_ldexpf(ntau, -rE[qb]);
+    s_init[qb] = PS ? f32x4{nt_e[qb], nt_e[qb], nt_e[qb], nt_e[qb]} : f32x4{0.f, 0.f, 0.f, 0.f};
     dw_init[qb] = f32x4{nxd, nxd, nxd, nxd};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -864,14 +913,17 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       qf[qb][ks] = ok ? ld16(Q + (int64_t)row * p.qsn + col) : zero_bf16x8();
       dof[qb][ks] = ok ? ld16(dO + (int64_t)row * p.dosn + col) : zero_bf16x8();
       if (XT && ok) {
-        *reinterpret_cast<bf16x8*>(Qx + (int64_t)row * D + col) = scale_frag(qf[qb][ks], rX[qb]);
-        *reinterpret_cast<bf16x8*>(dOx + (int64_t)row * D + col) = scale_frag(dof[qb][ks], rX[qb]);
+        const int64_t o = (int64_t)row * D + col;
+        *reinterpret_cast<bf16x8*>(Qx + o) =
+            scale_frag(qf[qb][ks], __builtin_amdgcn_ldexpf(rX[qb], 9 * rE[qb]));
+        *reinterpret_cast<bf16x8*>(dOx + o) =
+            scale_frag(dof[qb][ks], __builtin_amdgcn_ldexpf(rX[qb], 10 * rE[qb]));
+        *reinterpret_cast<bf16x8*>(Qs + o) = scale_frag(qf[qb][ks], __builtin_amdgcn_ldexpf(1.f, -rE[qb]));
       }
-      if (PS) qf[qb][ks] = scale_frag(qf[qb][ks], scale);
+      if (PS) qf[qb][ks] = scale_frag(qf[qb][ks], sc_e[qb]);  // a power of two: exact
     }
   }
 
-  const f32x4 s_init = PS ? f32x4{ntau, ntau, ntau, ntau} : f32x4{0.f, 0.f, 0.f, 0.f};
   int cnt[QB] = {};  // lane-local tie counts (first pass)
   // Sum of every ds the wave forms, accumulated by the MFMA: a constant A fragment whose
   // row 0 is all ones turns the ds^T operand into its column sums (lanes g == 0, slot 0).
@@ -940,7 +992,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
           }
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) {
-            f32x4 a4 = s_init, c4 = dw_init[qb];
+            f32x4 a4 = s_init[qb], c4 = dw_init[qb];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
               a4 = mfma16x16x32(kf[ks], qf[qb][ks], a4);
@@ -950,7 +1002,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
             dw[kk][qb] = c4;
           }
         }
-        affine_kq<PS>(s, scale, ntau);
+        affine_kq_rows<PS>(s, sc_e, nt_e);
         if (masked) mask_kq(s, n0, hf, qrow0, N, CAUSAL, g, r16);
         if (any_peak_tie(s, rM, rG)) {
           ds_kq<true>(s, dw, cnt, rM, rG);
@@ -996,10 +1048,11 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
     const int qrow = qrow0 + 16 * qb + r16;
     if (g == 0 && qrow < N) {
       // G''/Nmax for the dK/dV kernel with the row-scaled tiles (D <= 64), else G/Nmax
-      rc_plane(p, bh, 7)[qrow] = c > 0 ? (XT ? rG[qb] : rG[qb] * (ds_mult * rX[qb])) / (float)c : 0.f;
+      // G'' 2^-9e / Nmax for the dK/dV kernel's peak-normalised form (D <= 64), else G/Nmax
+      rc_plane(p, bh, 7)[qrow] = c > 0 ? (XT ? rG[qb] : rG0[qb] * (ds_mult * rX[qb])) / (float)c : 0.f;
       double rs = (double)adt[qb][0];
       if (c > 1) rs -= (double)rG[qb] * (double)(c - 1);
-      dsum += rs * (double)rX[qb];
+      dsum += rs * (double)__builtin_amdgcn_ldexpf(rX[qb], 9 * rE[qb]);
     }
     multi = multi || (c > 1 && rG[qb] != 0.f);
     rG[qb] = c > 0 ? rG[qb] / (float)c : 0.f;  // for a second pass
@@ -1020,7 +1073,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int qrow = qrow0 + 16 * qb + r16;
-    const float rowf = ds_mult * rX[qb];
+    const float rowf = ds_mult * __builtin_amdgcn_ldexpf(rX[qb], 9 * rE[qb]);
     if (qrow < N) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
@@ -1058,6 +1111,20 @@ __device__ __forceinline__ void affine_qk(f32x4 (&s)[2][KB], float scale, float 
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) s[qq][kb][i] = __builtin_fmaf(s[qq][kb][i], scale, ntau);
+}
+
+// affine_qk with a -tau per query row (register i of block qq): the peak-normalised scores of
+// the D <= 64 form, formed from Q 2^-e.
+template <int KB, bool PS>
+__device__ __forceinline__ void affine_qk_rows(f32x4 (&s)[2][KB], float scale,
+                                               const f32x4 (&ntau)[2]) {
+  if (PS) return;
+#pragma unroll
+  for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[qq][kb][i] = __builtin_fmaf(s[qq][kb][i], scale, ntau[qq][i]);
 }
 
 template <int KB>
@@ -1104,9 +1171,10 @@ __device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], c
   }
 }
 
-// D <= 64 form (Q and dO tiles also staged scaled by x = g/Z): the dV weight u^10 over s and
-// dS/(10 scale x) = u^9 dw + [u == M] G''/Nmax over dw = dW - D.  rc holds the planes
-// (M, -D, G''/Nmax).
+// D <= 64 form: the scores are peak-normalised (scaled by 2^-e per row, see pow9_unit) and
+// the Q and dO tiles of the dK and dV products are staged scaled by x 2^9e and x 2^10e.  The
+// dV weight u^10 over s and dS/(10 scale x 2^9e) = u^9 dw + [u == M] G''/Nmax over
+// dw = dW - D, in the scaled units.  rc holds the planes (M 2^-e, -D, G'' 2^-9e/Nmax).
 template <int KB>
 __device__ __forceinline__ void w_ds_qk_x(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const float* rc,
                                           int pitch, int r4) {
@@ -1118,12 +1186,10 @@ __device__ __forceinline__ void w_ds_qk_x(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB],
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        const float u = relu_mfma(s[qq][kb][i]);
-        const float u2 = u * u;
-        const float u4 = u2 * u2;
-        const float u9 = u4 * u4 * u;
-        s[qq][kb][i] = u9 * u;
-        const float tie = (u == m4[i]) ? t4[i] : 0.f;  // G'' = 0 on silent rows
+        const float sv = s[qq][kb][i];
+        const float u9 = pow9_unit(sv);
+        s[qq][kb][i] = u9 * sv;                           // 0 for sv <= 0 (u9 = 0)
+        const float tie = (sv == m4[i]) ? t4[i] : 0.f;  // M > 0; G'' = 0 on silent rows
         dw[qq][kb][i] = __builtin_fmaf(u9, dw[qq][kb][i], tie);
       }
   }
@@ -1138,11 +1204,9 @@ __device__ __forceinline__ void w_ds_qk_x_notie(f32x4 (&s)[2][KB], f32x4 (&dw)[2
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        const float u = relu_mfma(s[qq][kb][i]);
-        const float u2 = u * u;
-        const float u4 = u2 * u2;
-        const float u9 = u4 * u4 * u;
-        s[qq][kb][i] = u9 * u;
+        const float sv = s[qq][kb][i];
+        const float u9 = pow9_unit(sv);
+        s[qq][kb][i] = u9 * sv;
         dw[qq][kb][i] = u9 * dw[qq][kb][i];
       }
 }
@@ -1213,8 +1277,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   // (M, rho, kappa, -kappa D, G/Nmax) of the tile's rows: a lane reads the four consecutive
   // rows its registers cover as one f32x4 per plane (broadcast within a 16-lane group; the
   // four groups' rows are 8 apart, in different banks).
-  // XT: three planes (M, -D, G''/Nmax).
-  constexpr int NPL = XT ? 3 : 5;
+  // XT: four planes (M 2^-e, -D, G'' 2^-9e/Nmax, -tau 2^-e) of the peak-normalised form.
+  constexpr int NPL = XT ? 4 : 5;
   constexpr int XS = XT ? BMQ * DK : 8;  // scaled tiles (unused at D = 128)
   __shared__ __attribute__((aligned(16))) bf16 Qs0[BMQ * DK];
   __shared__ __attribute__((aligned(16))) bf16 dOs0[BMQ * DK];
@@ -1239,12 +1303,16 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const bf16* V = static_cast<const bf16*>(p.v) + b * p.vsb + h * p.vsh;
   const bf16* dO = static_cast<const bf16*>(p.dout) + b * p.dosb + h * p.dosh;
   // Staging of the row constants: wave w copies plane w of the tile's rows (XT: workspace
-  // planes 0, 1, 7 = M, -D, G''/Nmax; else 0, 4, 5, 6, 7 = M, rho, kappa, -kappa D, G/Nmax,
-  // wave 0 also the last).
-  const float* RCgw = rc_plane(p, bh, XT ? (w == 2 ? 7 : w) : (w == 0 ? 0 : 3 + w));
+  // planes 4, 1, 7, 5 = M 2^-e, -D, G'' 2^-9e/Nmax, -tau 2^-e; else 0, 4, 5, 6, 7 = M, rho,
+  // kappa, -kappa D, G/Nmax, wave 0 also the last).
+  const float* RCgw = rc_plane(p, bh, XT ? (w == 0 ? 4 : w == 2 ? 7 : w == 3 ? 5 : 1)
+                                         : (w == 0 ? 0 : 3 + w));
   const float* RCg4 = rc_plane(p, bh, 7);
+  // XT: the scaled copies written by the dQ kernel (Q 2^-e for the scores, Q x 2^9e and
+  // dO x 2^10e for the dK and dV products)
   const bf16* Qx = XT ? static_cast<const bf16*>(p.qx) + (int64_t)bh * N * D : nullptr;
   const bf16* dOx = XT ? static_cast<const bf16*>(p.dox) + (int64_t)bh * N * D : nullptr;
+  const bf16* Qsc = XT ? static_cast<const bf16*>(p.qs) + (int64_t)bh * N * D : nullptr;
   // The workgroup's 64-key tiles.  With the tile activity of the dQ stage, workgroup j of a
   // (b, h) takes positions TPW j .. TPW j + TPW - 1 of the order "active tiles ascending, then
   // silent tiles": active tiles share workgroups, so no wave idles beside an active one, and
@@ -1308,15 +1376,19 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const int tie_bit = p.amap ? 2 << (((KPW * w) % 64) / 32) : 0xff;
 
   // Tiles go straight from global memory to LDS buffer bb; rows >= N repeat row N - 1 (their
-  // scores are masked), including their row constants.
-  // (The register-lean clamped loads: this kernel is at the register limit.)
-  const TileDma<D, DK> tdma(w, lane, 0);
+  // scores are masked), including their row constants.  D <= 64: whole tiles take a scalar
+  // base plus the lanes' fixed 32-bit offsets (the scaled copies share one set: both have row
+  // stride D); D = 128, at the register limit, forms every address from the row and column.
+  const TileDma<D, DK> tq(w, lane, p.qsn), tdo(w, lane, p.dosn), tx(w, lane, D);
   auto load_tile = [&](int m, const QBuf& bb) {
-    tdma.load_clamped(Q, p.qsn, m, N, bb.q, w);
-    tdma.load_clamped(dO, p.dosn, m, N, bb.o, w);
     if (XT) {
-      tdma.load_clamped(Qx, D, m, N, bb.qx, w);
-      tdma.load_clamped(dOx, D, m, N, bb.ox, w);
+      tx.load(Qsc, D, m, N, bb.q, w);
+      tdo.load(dO, p.dosn, m, N, bb.o, w);
+      tx.load(Qx, D, m, N, bb.qx, w);
+      tx.load(dOx, D, m, N, bb.ox, w);
+    } else {
+      tq.load_clamped(Q, p.qsn, m, N, bb.q, w);
+      tq.load_clamped(dO, p.dosn, m, N, bb.o, w);
     }
     const int row = min(m + lane, N - 1);
     if (w < NPL) lds_dma4(RCgw + row, bb.rc + w * BMQ);
@@ -1358,11 +1430,16 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         if (!(code & 1)) continue;          // a silent 32-row half
         const bool ties = (code & tie_bit) != 0;
         f32x4 s[2][KB], dw[2][KB];
+        f32x4 ntr[2];  // XT: -tau 2^-e of the lane's rows in each 16-row block
 #pragma unroll
         for (int qq = 0; qq < 2; ++qq) {
-          // XT: the dW accumulator starts at -D of the four rows the lane's registers cover
-          const f32x4 dw0 = XT ? *reinterpret_cast<const f32x4*>(bc.rc + BMQ + 32 * hf + 8 * g + 4 * qq)
+          // XT: the dW accumulator starts at -D of the four rows the lane's registers cover,
+          // the score accumulator at their -tau 2^-e (scale folded into K) or 0 (affine below)
+          const int r4 = 32 * hf + 8 * g + 4 * qq;
+          const f32x4 dw0 = XT ? *reinterpret_cast<const f32x4*>(bc.rc + BMQ + r4)
                                : f32x4{0.f, 0.f, 0.f, 0.f};
+          if (XT) ntr[qq] = *reinterpret_cast<const f32x4*>(bc.rc + 3 * BMQ + r4);
+          const f32x4 sa0 = (XT && PS) ? ntr[qq] : s_init;
           bf16x8 qa[KS], da[KS];
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
@@ -1372,7 +1449,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
           }
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb) {
-            f32x4 a4 = s_init, c4 = dw0;
+            f32x4 a4 = sa0, c4 = dw0;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
               a4 = mfma16x16x32(qa[ks], kf[kb][ks], a4);
@@ -1382,7 +1459,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
             dw[qq][kb] = c4;
           }
         }
-        affine_qk<KB, PS>(s, scale, ntau);
+        if (XT) affine_qk_rows<KB, PS>(s, scale, ntr);
+        else affine_qk<KB, PS>(s, scale, ntau);
         if (masked) mask_qk<KB>(s, m0, hf, kw0, N, CAUSAL, g, r16);
         // rows 32 hf + 8 g + 4 qq + (0..3) of the tile are perm_row(2 hf + qq, 4 g + i)
         if constexpr (XT) {
