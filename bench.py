@@ -22,7 +22,8 @@ Also measured in the same run and reported on the same JSON line:
   causal_fir at C2, and the numpy flash restatement on C4 slices extrapolated to a step.
 
 ``--only MODE`` runs one workload alone and prints its own JSON (for rocprofv3 passes and
-per-stage timing): flash (C4 step), flash_c5 (C5 step), fir, copy (512 MiB device copy, the
+per-stage timing): flash (C4 step), flash_c5 (C5 step), fir, fir_sweep (the FIR and a device
+copy from 32 to 512 MiB per launch), copy (512 MiB device copy, the
 counter calibration), rows (row-fused score kernels on the C3 scores), lm (C3 LM step),
 mha6 (the 6-layer stack), ref (the reference's published shapes), kernels (per-stage HIP
 events at C4, C4 50 % silent and C5).
@@ -166,11 +167,14 @@ def kernel_times(q, k, v, dO, tau_val, iters):
     return out
 
 
-def bench_fir(dev, reps=200, pairs=20):
+def bench_fir(dev, reps=200, pairs=20, B=8):
+    """C2 (B = 8: K [8, 8, 2048, 64] bf16, 7 per-head taps) forward FIR, GB/s, over `pairs`
+    distinct input/output buffers, beside a device copy of the same bytes; other B scale the
+    bytes per launch with the same per-slice shape (the size sweep)."""
     from paper_01_anti_decoy_pnfirtau_amd import ops  # noqa: F401
 
     g = torch.Generator().manual_seed(7)
-    xs = [torch.randn(8, 8, 2048, 64, generator=g).to(torch.bfloat16).to(dev) for _ in range(pairs)]
+    xs = [torch.randn(B, 8, 2048, 64, generator=g).to(torch.bfloat16).to(dev) for _ in range(pairs)]
     ys = [torch.empty_like(x) for x in xs]
     t = torch.rand(8, 7, generator=g)
     taps = (t / t.sum(-1, keepdim=True)).to(dev)
@@ -182,7 +186,7 @@ def bench_fir(dev, reps=200, pairs=20):
         x, y = xs[i % pairs], ys[i % pairs]
         st = torch.cuda.current_stream().cuda_stream
         rc = L.pnfx_fir_fwd(x.data_ptr(), x.stride(0), x.stride(1), x.stride(2), y.data_ptr(),
-                            8, 8, 2048, 64, taps.data_ptr(), 8, 7, _lib.PNFX_BF16, st)
+                            B, 8, 2048, 64, taps.data_ptr(), 8, 7, _lib.PNFX_BF16, st)
         _lib.check(rc, "pnfx_fir_fwd")
 
     for i in range(pairs):
@@ -204,7 +208,7 @@ def bench_fir(dev, reps=200, pairs=20):
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) / (rounds * pairs) * 1e3
-    nbytes = 2 * 8 * 8 * 2048 * 64 * 2
+    nbytes = 2 * B * 8 * 2048 * 64 * 2
     gbps = nbytes / (us * 1e-6) / 1e9
     # reference point: a plain device copy of the same bytes over the same buffers
     cgraph = torch.cuda.CUDAGraph()
@@ -220,9 +224,26 @@ def bench_fir(dev, reps=200, pairs=20):
     torch.cuda.synchronize()
     cus = e0.elapsed_time(e1) / (rounds * pairs) * 1e3
     return {"us_per_launch": round(us, 3), "bytes": nbytes, "gbps": round(gbps, 1),
-            "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4), "buffers": f"{pairs} pairs x 32 MiB",
+            "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
+            "buffers": f"{pairs} pairs x {nbytes >> 20} MiB",
             "same_bytes_copy_us": round(cus, 3),
             "same_bytes_copy_gbps": round(nbytes / (cus * 1e-6) / 1e9, 1)}
+
+
+def bench_fir_sweep(dev):
+    """The FIR and a same-byte device copy from C2's 32 MiB per launch up to 512 MiB (batch 8
+    to 128 of [8, 2048, 64] slices), with at least 640 MiB of distinct buffers per size so that
+    the 256 MiB Infinity Cache serves no repeats: where the small-launch floor lies."""
+    out = {}
+    for B in (8, 16, 32, 64, 128):
+        pairs = max(2, 20 * 8 // B)
+        r = bench_fir(dev, reps=max(20, 200 * 8 // B), pairs=pairs, B=B)
+        out[f"{r['bytes'] >> 20}MiB"] = {
+            "fir_us": r["us_per_launch"], "fir_gbps": r["gbps"], "fir_frac_hbm": r["frac_hbm"],
+            "copy_us": r["same_bytes_copy_us"], "copy_gbps": r["same_bytes_copy_gbps"],
+            "copy_frac_hbm": round(r["same_bytes_copy_gbps"] / PEAK_HBM_GBPS, 4)}
+        torch.cuda.empty_cache()
+    return out
 
 
 def bench_rows(dev, reps=20):
@@ -524,7 +545,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["flash", "flash_c5", "fir", "copy", "lm", "mha6", "ref",
+    ap.add_argument("--only", choices=["flash", "flash_c5", "fir", "fir_sweep", "copy", "lm", "mha6", "ref",
                                        "kernels", "rows"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -539,6 +560,9 @@ def main():
 
     if args.only == "copy":
         print(json.dumps(bench_copy(dev)))
+        return
+    if args.only == "fir_sweep":
+        print(json.dumps({"fir_size_sweep": bench_fir_sweep(dev)}), flush=True)
         return
     if args.only == "fir":
         print(json.dumps(bench_fir(dev, reps=100)))
