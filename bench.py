@@ -17,13 +17,16 @@ Also measured in the same run and reported on the same JSON line:
   taps) in GB/s, rotating 20 input/output buffer pairs (640 MiB) so the 256 MB
   Infinity Cache cannot serve repeats;
 * ``wide_head``: config C5 (B=8, H=8, N=4096, d=128) TFLOP/s;
+* ``flash_fp32``: the fp32 flash path (B=1, H=8, N=2048, d=64), ms per fwd+bwd step;
+* ``fir_fused_forward``: C4 forward from raw keys, FIR + flash forward against the forward
+  with the FIR fused into its key-tile load;
 * ``cpu_baseline``: the reference's CPU path on this host's cores -- the eager
   PnFirTauMHA fp32 forward + backward at config C1 (the headline CPU figure), the eager
   causal_fir at C2, and the numpy flash restatement on C4 slices extrapolated to a step.
 
 ``--only MODE`` runs one workload alone and prints its own JSON (for rocprofv3 passes and
 per-stage timing): flash (C4 step), flash_c5 (C5 step), fir, fir_sweep (the FIR and a device
-copy from 32 to 512 MiB per launch), copy (512 MiB device copy, the
+copy from 32 to 512 MiB per launch), fir_fused (FIR + forward against the fused forward), copy (512 MiB device copy, the
 counter calibration), rows (row-fused score kernels on the C3 scores), lm (C3 LM step),
 mha6 (the 6-layer stack), ref (the reference's published shapes), kernels (per-stage HIP
 events at C4, C4 50 % silent and C5).
@@ -244,6 +247,32 @@ def bench_fir_sweep(dev):
             "copy_frac_hbm": round(r["same_bytes_copy_gbps"] / PEAK_HBM_GBPS, 4)}
         torch.cuda.empty_cache()
     return out
+
+
+def bench_fir_fused(dev, steps=20, warmup=5):
+    """Forward only (inference) at C4 with raw keys: the causal FIR then the flash forward
+    (two launches, src/pnfirtau_attention.py:299-315) against the forward with the FIR fused
+    into its key-tile load (pnfx_flash_fwd_fir).  The outputs are bitwise equal
+    (tests/test_gpu_fused_fir.py)."""
+    from paper_01_anti_decoy_pnfirtau_amd import ops
+    from paper_01_anti_decoy_pnfirtau_amd.pnfirtau_attention import causal_gaussian_taps
+
+    B, H, N, D = C4["B"], C4["H"], C4["N"], C4["D"]
+    q, kraw, v, _ = make_inputs(B, H, N, D, 3, dev)
+    taps = causal_gaussian_taps(7).to(dev)
+    t32 = torch.tensor(0.0, device=dev)
+
+    def two():
+        k = torch.ops.pnfx.fir_fwd(kraw, taps)
+        torch.ops.pnfx.flash_fwd(q, k, v, t32, D ** -0.5, 0.5, True, True, False, False)
+
+    def fused():
+        ops.flash_fwd_fused_fir(q, kraw, v, t32, taps, D ** -0.5, 0.5, True, True)
+
+    w2, e2 = time_steps(two, steps, warmup)
+    wf, ef = time_steps(fused, steps, warmup)
+    return {"config": "C4 forward, raw keys, tau = 0", "fir_then_flash_ms": round(e2, 4),
+            "fused_fir_flash_ms": round(ef, 4), "fused_over_two_launches": round(ef / e2, 3)}
 
 
 def bench_rows(dev, reps=20):
@@ -545,7 +574,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["flash", "flash_c5", "fir", "fir_sweep", "copy", "lm", "mha6", "ref",
+    ap.add_argument("--only", choices=["flash", "flash_c5", "fir", "fir_sweep", "fir_fused", "copy", "lm", "mha6", "ref",
                                        "kernels", "rows"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -563,6 +592,9 @@ def main():
         return
     if args.only == "fir_sweep":
         print(json.dumps({"fir_size_sweep": bench_fir_sweep(dev)}), flush=True)
+        return
+    if args.only == "fir_fused":
+        print(json.dumps(bench_fir_fused(dev)), flush=True)
         return
     if args.only == "fir":
         print(json.dumps(bench_fir(dev, reps=100)))
@@ -630,6 +662,14 @@ def main():
     kern5 = kernel_times(q5, k5, v5, dO5, 0.0, max(3, args.steps // 4))
     del q5, k5, v5, dO5
 
+    # fp32 flash (the parity path: one lane per query row, scalar FMA, no MFMA)
+    F32 = dict(B=1, H=8, N=2048, D=64)
+    qf, kf, vf, dOf = (t.float() for t in make_inputs(F32["B"], F32["H"], F32["N"], F32["D"], 2, dev))
+    wallf, _ = time_steps(flash_step_fn(qf, kf, vf, dOf, 0.0), 5, 2)
+    flopsf = 7 * gemm_flops(F32["B"], F32["H"], F32["N"], F32["D"])
+    del qf, kf, vf, dOf
+
+    fir_fused = bench_fir_fused(dev)
     lm = bench_lm(dev)
     mha6 = bench_mha6(dev)
     refcfg = bench_reference_configs(dev)
@@ -668,6 +708,11 @@ def main():
         "wide_head": {"config": C5, "ms_per_step": round(wall5, 4),
                       "tflops": round(flops5 / (wall5 * 1e-3) / 1e12, 2),
                       "kernel_ms": {n: r["ms"] for n, r in kern5.items()}},
+        "flash_fp32": {"config": F32, "ms_per_step": round(wallf, 4),
+                       "tflops": round(flopsf / (wallf * 1e-3) / 1e12, 3),
+                       "path": "fp32 parity kernels (csrc/flash_f32.hip): one lane per query row, "
+                               "scalar FMA, no MFMA"},
+        "fir_fused_forward": fir_fused,
         "lm_step": lm,
         "mha6_stack": mha6,
         "reference_configs": refcfg,

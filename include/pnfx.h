@@ -127,6 +127,25 @@ int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const v
                    int64_t N, int64_t D, const float* tau, float scale, float gamma,
                    int has_gamma, int causal, int dtype, void* stream);
 
+/*
+ * pnfx_flash_fwd with the causal FIR of the keys fused into the kernel's key-tile load:
+ * k_raw holds the raw (pre-FIR) keys, taps / taps_rows / K are those of pnfx_fir_fwd
+ * (K <= 7), and every key tile is filtered in LDS from its raw rows and 6-row halo with
+ * pnfx_fir_fwd's arithmetic, so O, o_lo, M, Z and the tile mask are bitwise those of
+ * pnfx_fir_fwd followed by pnfx_flash_fwd.  bf16, D = 64, no tie counts, no silent-tile
+ * bound.  Replaces src/pnfirtau_attention.py:299-315's separate causal_fir +
+ * flash_pn_fir_tau_attention launches for a forward that needs no filtered keys afterwards;
+ * it filters every key tile once per query block that reads it, which measures slower than
+ * the two launches (the modules use those).
+ */
+int pnfx_flash_fwd_fir(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k_raw,
+                       int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
+                       int64_t vsh, int64_t vsn, void* o, int64_t osb, int64_t osh, int64_t osn,
+                       void* o_lo, float* M, float* Z, uint8_t* tile_mask, int64_t B,
+                       int64_t H, int64_t N, int64_t D, const float* tau, float scale,
+                       float gamma, int has_gamma, int causal, const float* taps,
+                       int64_t taps_rows, int K, int dtype, void* stream);
+
 /* Bytes of the optional pnfx_flash_fwd workspace for this shape (the per-tile key
  * norms of its silent-tile bound).  No counterpart in the reference. */
 int64_t pnfx_flash_fwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D);

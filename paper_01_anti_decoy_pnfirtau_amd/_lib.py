@@ -40,6 +40,10 @@ def _declare(lib: ctypes.CDLL) -> None:
             [vp, i64, i64, i64] * 4
             + [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, f32, f32, i32, i32, i32, vp],
             i32),
+        "pnfx_flash_fwd_fir": (
+            [vp, i64, i64, i64] * 4
+            + [vp, vp, vp, vp, i64, i64, i64, i64, vp, f32, f32, i32, i32, vp, i64, i32, i32, vp],
+            i32),
         "pnfx_flash_fwd_workspace_size": ([i64, i64, i64, i64], i64),
         "pnfx_flash_bwd_workspace_size": ([i64, i64, i64, i64], i64),
         "pnfx_flash_bwd": (
@@ -85,7 +89,8 @@ def exported_symbols() -> list[str]:
     """Names of every entry point include/pnfx.h declares."""
     return [
         "pnfx_abi_version", "pnfx_last_error", "pnfx_fir_fwd", "pnfx_fir_bwd",
-        "pnfx_pn_rows_fwd", "pnfx_pn_rows_bwd", "pnfx_flash_fwd", "pnfx_flash_fwd_workspace_size",
+        "pnfx_pn_rows_fwd", "pnfx_pn_rows_bwd", "pnfx_flash_fwd", "pnfx_flash_fwd_fir",
+        "pnfx_flash_fwd_workspace_size",
         "pnfx_flash_bwd_workspace_size", "pnfx_flash_bwd", "pnfx_flash_bwd_stages",
         "pnfx_flash_bwd_noalloc",
     ]

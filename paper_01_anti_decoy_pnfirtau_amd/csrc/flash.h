@@ -19,6 +19,10 @@ struct FwdParams {
   const float* tau;
   float scale, gamma;
   int has_gamma;
+  // pnfx_flash_fwd_fir: k holds the raw keys and the kernel filters each key tile with these
+  // causal FIR taps ([fir_taps_rows][fir_k] fp32, as pnfx_fir_fwd) before its scores
+  const float* fir_taps = nullptr;
+  int fir_taps_rows = 0, fir_k = 0;
 };
 
 struct BwdParams {
@@ -77,6 +81,7 @@ struct BwdWorkspace {
 };
 
 int flash_fwd_bf16(const FwdParams& fp, int64_t D, bool causal, hipStream_t st);
+int flash_fwd_fir_bf16(const FwdParams& fp, int64_t D, bool causal, hipStream_t st);
 int flash_bwd_bf16(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, int stages,
                    hipStream_t st);
 int flash_fwd_f32(const FwdParams& fp, int64_t D, bool causal, bool has_gamma, hipStream_t st);

@@ -180,10 +180,12 @@ struct TileDma {
 __device__ __forceinline__ void lds_dma4(const float* src, float* dst) {
   __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
 }
-// One LDS buffer of the forward and dQ kernels: a key tile of K and V.
+// One LDS buffer of the forward and dQ kernels: a key tile of K and V (and, for the forward
+// with the FIR fused into its key-tile load, the tile's raw key rows).
 struct KVBuf {
   bf16* k;
   bf16* v;
+  bf16* kr = nullptr;
 };
 
 // One LDS buffer of the dK/dV kernel: a query tile of Q and dO, for D <= 64 also of their
@@ -403,20 +405,28 @@ __device__ __forceinline__ float max_nonneg(float a, float b) {
 constexpr int kMaxListTiles = 1024;
 
 // COUNT: also count the peak ties (Nmax); the training path leaves that to the backward.
-template <int D, bool CAUSAL, bool PS, bool COUNT>
-__global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdParams p) {
+// FIRK (D = 64 only): p.k holds the raw keys, and each key tile is filtered in LDS (the causal
+// FIR of pnfx_fir_fwd, fused into the key-tile load) before its scores; see
+// pnfx_flash_fwd_fir.
+template <int D, bool CAUSAL, bool PS, bool COUNT, bool FIRK = false>
+__global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kernel(FwdParams p) {
   constexpr int BM = 128, BN = 64;
-  constexpr bool BOUND = D <= 64;  // the silent-tile bound (see flash_key_norm_kernel)
+  constexpr bool BOUND = D <= 64 && !FIRK;  // the silent-tile bound (see flash_key_norm_kernel)
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
+  static_assert(!FIRK || D == 64, "the fused FIR is built for d = 64");
   // Two K/V tile buffers as separate LDS objects (see the dK/dV kernel), filled straight
   // from global memory.
   __shared__ __attribute__((aligned(16))) bf16 Ks0[BN * DK];
   __shared__ __attribute__((aligned(16))) bf16 Vs0[BN * DK];
   __shared__ __attribute__((aligned(16))) bf16 Ks1[BN * DK];
   __shared__ __attribute__((aligned(16))) bf16 Vs1[BN * DK];
-  const KVBuf buf0{Ks0, Vs0}, buf1{Ks1, Vs1};
+  // FIRK: the raw key rows n0 - 8 .. n0 + 63 of each tile, row-major [72][64]
+  constexpr int KR_ROWS = 72;
+  __shared__ __attribute__((aligned(16))) bf16 Kr0[FIRK ? KR_ROWS * DK : 8];
+  __shared__ __attribute__((aligned(16))) bf16 Kr1[FIRK ? KR_ROWS * DK : 8];
+  const KVBuf buf0{Ks0, Vs0, Kr0}, buf1{Ks1, Vs1, Kr1};
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
@@ -541,8 +551,57 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
   // t is computed from the other; one barrier per tile.
   const TileDma<D, DK> kdma(w, lane, p.ksn), vdma(w, lane, p.vsn);
   auto load_tile = [&](int n, const KVBuf& bb) {
-    kdma.load(K, p.ksn, n, N, bb.k, w);
+    if constexpr (FIRK) {
+      // raw rows n - 8 .. n + 63, 8 chunks each (576 chunks: two per lane, a third for wave 0);
+      // rows outside [0, N) re-load a real row (the filter skips rows before 0, and keys past
+      // N are masked)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        if (j == 2 && w != 0) break;
+        const int L = j * 256 + w * 64 + lane;
+        const int r = min(max(n - 8 + (L >> 3), 0), N - 1);
+        lds_dma16(K + (int64_t)r * p.ksn + 8 * (L & 7), bb.kr + (j * 256 + w * 64) * 8);
+      }
+    } else {
+      kdma.load(K, p.ksn, n, N, bb.k, w);
+    }
     vdma.load(V, p.vsn, n, N, bb.v, w);
+  };
+  // FIRK: the filter taps of this head, h[u] = taps[K - 1 - u] (scalar registers)
+  float fh[7] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if constexpr (FIRK) {
+    const float* tp = p.fir_taps + (p.fir_taps_rows == 1 ? 0 : h) * p.fir_k;
+#pragma unroll
+    for (int u = 0; u < 7; ++u) fh[u] = u < p.fir_k ? tp[p.fir_k - 1 - u] : 0.f;
+  }
+  // FIRK: the filtered key tile n0 .. n0 + 63 formed in bc.k from the raw rows in bc.kr, with
+  // pnfx_fir_fwd's arithmetic (an fp32 FMA chain in lag order, one bf16 rounding): thread tid
+  // forms rows r0, r0 + 1 (r0 = 2 (tid / 8)) of chunk tid % 8.
+  auto filter_tile = [&](int n0, const KVBuf& bc) {
+    const int c = tid & 7, r0 = 2 * (tid >> 3);
+    u32x4 x[8];  // raw rows n0 + r0 - 6 .. n0 + r0 + 1
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = *reinterpret_cast<const u32x4*>(bc.kr + (r0 + 2 + i) * DK + 8 * c);
+    const auto elem = [](const u32x4& v, int e) {
+      const uint32_t d = v[e >> 1];
+      return __uint_as_float((e & 1) ? (d & 0xffff0000u) : (d << 16));
+    };
+#pragma unroll
+    for (int o = 0; o < 2; ++o) {
+      const int n = n0 + r0 + o;
+      float acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = elem(x[o + 6], e) * fh[0];
+#pragma unroll
+      for (int u = 1; u < 7; ++u)
+        if (u < p.fir_k && n - u >= 0)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(elem(x[o + 6 - u], e), fh[u], acc[e]);
+      bf16x8 y;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = (bf16)acc[e];
+      *reinterpret_cast<bf16x8*>(bc.k + rt_off<DK>(r0 + o, c)) = y;
+    }
   };
   // Entry e of the list: tile t, computed from buffer bc while the next entry's tile tn
   // streams into buffer bn.
@@ -556,6 +615,10 @@ __global__ __launch_bounds__(256, D <= 64 ? 3 : 2) void flash_fwd_kernel(FwdPara
     wait_vmem();  // this wave's part of tile t is in LDS
     __syncthreads();
     if (e + 1 < nlist) load_tile(tn * BN, bn);
+    if constexpr (FIRK) {  // the filtered tile, published by a second barrier
+      filter_tile(n0, bc);
+      __syncthreads();
+    }
     // the wave's own bound (the tile norm is wave-uniform: a scalar register)
     const bool bounded = bound && qb_w * i2f(__builtin_amdgcn_readfirstlane(f2i(kn[t]))) <= tau;
     bool active = false;
@@ -1605,6 +1668,20 @@ void launch_fwd_dp(const FwdParams& fp, bool causal, hipStream_t st) {
   }
 }
 
+int flash_fwd_fir_launch(const FwdParams& fp, bool causal, hipStream_t st) {
+  const int nqb = (fp.N + 127) / 128;
+  const dim3 grid((unsigned)(nqb * fp.B * fp.H)), block(256);
+  const bool ps = pow2_scale(fp.scale);
+  if (causal) {
+    if (ps) hipLaunchKernelGGL((flash_fwd_kernel<64, true, true, false, true>), grid, block, 0, st, fp);
+    else hipLaunchKernelGGL((flash_fwd_kernel<64, true, false, false, true>), grid, block, 0, st, fp);
+  } else {
+    if (ps) hipLaunchKernelGGL((flash_fwd_kernel<64, false, true, false, true>), grid, block, 0, st, fp);
+    else hipLaunchKernelGGL((flash_fwd_kernel<64, false, false, false, true>), grid, block, 0, st, fp);
+  }
+  return launch_status("pnfx_flash_fwd_fir");
+}
+
 template <int D>
 int launch_fwd_d(const FwdParams& fp, bool causal, hipStream_t st) {
   if (pow2_scale(fp.scale)) launch_fwd_dp<D, true>(fp, causal, st);
@@ -1674,6 +1751,14 @@ int flash_fwd_bf16(const FwdParams& fp, int64_t D, bool causal, hipStream_t st) 
   }
   set_error("flash: head dim %lld not in {16, 32, 64, 128}", (long long)D);
   return PNFX_EUNSUPPORTED;
+}
+
+int flash_fwd_fir_bf16(const FwdParams& fp, int64_t D, bool causal, hipStream_t st) {
+  if (D != 64) {
+    set_error("flash_fwd_fir: head dim %lld (the fused FIR is built for 64)", (long long)D);
+    return PNFX_EUNSUPPORTED;
+  }
+  return flash_fwd_fir_launch(fp, causal, st);
 }
 
 int flash_bwd_bf16(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, int stages,

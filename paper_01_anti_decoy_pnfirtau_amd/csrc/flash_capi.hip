@@ -118,6 +118,33 @@ extern "C" int pnfx_flash_fwd(const void* q, int64_t qsb, int64_t qsh, int64_t q
                             : flash_fwd_f32(fp, D, causal != 0, has_gamma != 0, st);
 }
 
+extern "C" int pnfx_flash_fwd_fir(const void* q, int64_t qsb, int64_t qsh, int64_t qsn,
+                                  const void* k_raw, int64_t ksb, int64_t ksh, int64_t ksn,
+                                  const void* v, int64_t vsb, int64_t vsh, int64_t vsn, void* o,
+                                  int64_t osb, int64_t osh, int64_t osn, void* o_lo, float* M,
+                                  float* Z, uint8_t* tile_mask, int64_t B, int64_t H, int64_t N,
+                                  int64_t D, const float* tau, float scale, float gamma,
+                                  int has_gamma, int causal, const float* taps, int64_t taps_rows,
+                                  int K, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_shape(B, H, N, D))) return rc;
+  PNFX_REQUIRE(dtype == PNFX_BF16, "flash_fwd_fir: bf16 only (dtype %d)", dtype);
+  if ((rc = check_operand("q", q, qsb, qsh, qsn, dtype))) return rc;
+  if ((rc = check_operand("k_raw", k_raw, ksb, ksh, ksn, dtype))) return rc;
+  if ((rc = check_operand("v", v, vsb, vsh, vsn, dtype))) return rc;
+  if ((rc = check_operand("o", o, osb, osh, osn, dtype))) return rc;
+  PNFX_REQUIRE(M && Z && tau && taps, "flash_fwd_fir: null statistics / tau / taps pointer");
+  PNFX_REQUIRE(!o_lo || aligned16(o_lo), "flash_fwd_fir: o_lo is a 16-byte aligned bf16 buffer");
+  PNFX_REQUIRE(K >= 1 && K <= 7, "flash_fwd_fir: FIR length K=%d outside [1, 7]", K);
+  PNFX_REQUIRE(taps_rows == 1 || taps_rows == H, "flash_fwd_fir: taps_rows=%lld must be 1 or H=%lld",
+               (long long)taps_rows, (long long)H);
+  FwdParams fp{q, k_raw, v, o, o_lo, qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn,
+               M, Z, nullptr, tile_mask, nullptr, (int)B, (int)H, (int)N,
+               (int)((N + 31) / 32), (int)((N + 63) / 64), tau, scale, gamma, has_gamma != 0,
+               taps, (int)taps_rows, K};
+  return flash_fwd_fir_bf16(fp, D, causal != 0, reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" int64_t pnfx_flash_bwd_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D) {
   return BwdWorkspace(B, H, N, D).total();
 }

@@ -273,6 +273,34 @@ def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma:
     return o, o_lo, M, Z, Nm, mask
 
 
+def flash_fwd_fused_fir(q: Tensor, k_raw: Tensor, v: Tensor, tau: Tensor, taps: Tensor,
+                        scale: float, gamma: float, has_gamma: bool,
+                        causal: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Flash forward with the causal FIR of the keys fused into the key-tile load
+    (pnfx_flash_fwd_fir): k_raw are the keys before the FIR, taps as fir_fwd (fp32 [K] or
+    [H, K], K <= 7).  Returns (O, O_lo, M, Z, tile_mask), bitwise those of fir_fwd followed by
+    flash_fwd.  bf16, d = 64, inference only (no autograd, no tie counts): the filtered keys
+    are not materialised, so there is nothing for a backward to read."""
+    _check_qkv(q, k_raw, v)
+    B, H, N, D = q.shape
+    code = _code(q, "flash_fwd_fir")
+    q, k_raw, v = _bhnd(q, "q", True), _bhnd(k_raw, "k_raw", True), _bhnd(v, "v", True)
+    taps2 = taps.reshape(-1, taps.shape[-1]).to(device=q.device, dtype=torch.float32).contiguous()
+    o = _new_o(q, False)
+    o_lo = _new_o(q, False)
+    M = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
+    Z = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
+    mask = torch.empty(_mask_shape(B, H, N), device=q.device, dtype=torch.uint8)
+    t32 = _tau32(tau)
+    rc = _lib.lib().pnfx_flash_fwd_fir(
+        *_ptr4(q), *_ptr4(k_raw), *_ptr4(v), *_ptr4(o), o_lo.data_ptr(), M.data_ptr(),
+        Z.data_ptr(), mask.data_ptr() if mask.numel() else None, B, H, N, D, t32.data_ptr(),
+        scale, gamma, int(has_gamma), int(causal), taps2.data_ptr(), taps2.shape[0],
+        taps2.shape[1], code, _stream(q))
+    _lib.check(rc, "pnfx_flash_fwd_fir")
+    return o, o_lo, M, Z, mask
+
+
 @flash_fwd.register_fake
 def _(q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd, with_nmax):
     B, H, N, D = q.shape

@@ -143,6 +143,14 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
                                     *([None, 0, 0, 0] * 3), None, 4, 16, 16384, 64, None, 0.125,
                                     0.5, 1, 1, 1, None)
     assert rc == -1 and b"scratch" in lib.pnfx_last_error()
+    # the fused-FIR forward: bf16, d = 64 and K <= 7 only, refused before any device call
+    fake = ctypes.c_void_p(256)
+    args = ([fake, 64 * 8, 64 * 8, 64] * 4 + [fake, fake, fake, None, 1, 1, 8, 64, fake, 0.125,
+                                              0.5, 1, 1, fake, 1])
+    rc = lib.pnfx_flash_fwd_fir(*args, 8, 1, None)
+    assert rc == -1 and b"K=8" in lib.pnfx_last_error()
+    rc = lib.pnfx_flash_fwd_fir(*args, 7, 0, None)
+    assert rc == -1 and b"bf16 only" in lib.pnfx_last_error()
 
 
 def test_hip_ops_refuse_cpu_tensors():
