@@ -25,7 +25,8 @@ Also measured in the same run and reported on the same JSON line:
   causal_fir at C2, and the numpy flash restatement on C4 slices extrapolated to a step.
 
 ``--only MODE`` runs one workload alone and prints its own JSON (for rocprofv3 passes and
-per-stage timing): flash (C4 step), flash_c5 (C5 step), fir, fir_sweep (the FIR and a device
+per-stage timing): flash (C4 step), flash_c5 (C5 step), flash_silent (the C4 step with
+half the causal tiles silent), fir, fir_sweep (the FIR and a device
 copy from 32 to 512 MiB per launch), fir_fused (FIR + forward against the fused forward), copy (512 MiB device copy, the
 counter calibration), rows (row-fused score kernels on the C3 scores), lm (C3 LM step),
 mha6 (the 6-layer stack), ref (the reference's published shapes), kernels (per-stage HIP
@@ -574,8 +575,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["flash", "flash_c5", "fir", "fir_sweep", "fir_fused", "copy", "lm", "mha6", "ref",
-                                       "kernels", "rows"],
+    ap.add_argument("--only", choices=["flash", "flash_c5", "flash_silent", "fir", "fir_sweep", "fir_fused", "copy",
+                                       "lm", "mha6", "ref", "kernels", "rows"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -618,6 +619,12 @@ def main():
         flops5 = 7 * gemm_flops(C5["B"], C5["H"], C5["N"], C5["D"])
         print(json.dumps({"ms_per_step": wall5, "event_ms": ev5,
                           "tflops": flops5 / (wall5 * 1e-3) / 1e12}))
+        return
+    if args.only == "flash_silent":  # the C4 step with half the causal tiles silent, alone
+        qs_, ks_, vs_, dOs_ = make_inputs(C4["B"], C4["H"], C4["N"], C4["D"], 0, dev)
+        plant_silent(ks_, C4["N"])
+        walls, evs = time_steps(flash_step_fn(qs_, ks_, vs_, dOs_, 0.25), args.steps, args.warmup)
+        print(json.dumps({"ms_per_step": walls, "event_ms": evs}))
         return
     if args.only == "kernels":  # per-stage HIP-event times at C4 and C5
         out = {}
