@@ -13,6 +13,7 @@ pnfx::flash_fwd/_bwd   _FlashPnFirTauFn                 :814-968
 from __future__ import annotations
 
 import functools
+import math
 
 import torch
 from torch import Tensor
@@ -56,6 +57,8 @@ def _fir_call(x: Tensor, taps: Tensor, adjoint: bool) -> Tensor:
     if taps2.dtype != torch.float32 or not taps2.is_contiguous() or taps2.device != x.device:
         taps2 = taps2.to(device=x.device, dtype=torch.float32).contiguous()
     y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if y.numel() == 0:  # empty input: nothing to filter (the reference launches an empty grid)
+        return y
     fn = _lib.lib().pnfx_fir_bwd if adjoint else _lib.lib().pnfx_fir_fwd
     rc = fn(x4.data_ptr(), x4.stride(0), x4.stride(1), x4.stride(2), y.data_ptr(), B, H, N, C,
             taps2.data_ptr(), taps2.shape[0], taps2.shape[1], _code(x, "fir"), _stream(x))
@@ -103,12 +106,17 @@ def pn_rows_fwd(raw: Tensor, tau: Tensor, scale: float, p: float, gamma: float, 
                 causal: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Row-fused score -> weight over raw [..., N, N]; returns (W, M, Z, Nmax), stats per row."""
     N = raw.shape[-1]
-    r2 = raw.contiguous().view(-1, N)
-    R = r2.shape[0]
+    R = math.prod(raw.shape[:-1])
+    r2 = raw.contiguous().view(R, N)
     w = torch.empty_like(r2)
     M = torch.empty(R, device=raw.device, dtype=torch.float32)
     Z = torch.empty(R, device=raw.device, dtype=torch.float32)
     Nm = torch.empty(R, device=raw.device, dtype=torch.int32)
+    if r2.numel() == 0:  # no rows, or rows of length 0 (peak 0, mass 0 + 1e-12, no ties)
+        M.zero_()
+        Z.fill_(1e-12)
+        Nm.zero_()
+        return w.view(raw.shape), M, Z, Nm
     t32 = _tau32(tau)
     rc = _lib.lib().pnfx_pn_rows_fwd(r2.data_ptr(), N, w.data_ptr(), N, M.data_ptr(), Z.data_ptr(),
                                      Nm.data_ptr(), R, N, t32.data_ptr(), scale, p, gamma,
@@ -120,7 +128,7 @@ def pn_rows_fwd(raw: Tensor, tau: Tensor, scale: float, p: float, gamma: float, 
 
 @pn_rows_fwd.register_fake
 def _(raw, tau, scale, p, gamma, has_gamma, causal):
-    R = raw.numel() // max(raw.shape[-1], 1)
+    R = math.prod(raw.shape[:-1])
     f = lambda dt: torch.empty(R, device=raw.device, dtype=dt)  # noqa: E731
     # contiguous, as the real kernel returns it whatever raw's strides
     w = torch.empty(raw.shape, dtype=raw.dtype, device=raw.device)
@@ -133,11 +141,13 @@ def pn_rows_bwd(dw: Tensor, raw: Tensor, tau: Tensor, M: Tensor, Z: Tensor, Nmax
                 causal: bool) -> tuple[Tensor, Tensor]:
     """Backward of pn_rows_fwd: (d_raw, dtau_rows) with dtau_rows[r] = -sum_j du[r, j]."""
     N = raw.shape[-1]
-    r2 = raw.contiguous().view(-1, N)
-    g2 = dw.to(raw.dtype).contiguous().view(-1, N)
-    R = r2.shape[0]
+    R = math.prod(raw.shape[:-1])
+    r2 = raw.contiguous().view(R, N)
+    g2 = dw.to(raw.dtype).contiguous().view(R, N)
     d = torch.empty_like(r2)
     dt = torch.empty(R, device=raw.device, dtype=torch.float32)
+    if r2.numel() == 0:
+        return d.view(raw.shape), dt.zero_()
     t32 = _tau32(tau)
     rc = _lib.lib().pnfx_pn_rows_bwd(g2.data_ptr(), N, r2.data_ptr(), N, M.data_ptr(), Z.data_ptr(),
                                      Nmax.data_ptr(), d.data_ptr(), N, dt.data_ptr(), R, N,
@@ -149,7 +159,7 @@ def pn_rows_bwd(dw: Tensor, raw: Tensor, tau: Tensor, M: Tensor, Z: Tensor, Nmax
 
 @pn_rows_bwd.register_fake
 def _(dw, raw, tau, M, Z, Nmax, scale, p, gamma, has_gamma, causal):
-    R = raw.numel() // max(raw.shape[-1], 1)
+    R = math.prod(raw.shape[:-1])
     return (torch.empty(raw.shape, dtype=raw.dtype, device=raw.device),
             torch.empty(R, device=raw.device, dtype=torch.float32))
 
@@ -263,6 +273,8 @@ def flash_fwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, scale: float, gamma:
     buf = torch.empty(mbytes + nws, device=q.device, dtype=torch.uint8)
     mask = buf[:mn].view(mshape)
     ws = buf[mbytes:]
+    if B * H * N == 0:  # empty input: empty outputs, as the reference's empty launch grid gives
+        return o, o_lo, M, Z, Nm, mask
     t32 = _tau32(tau)
     rc = _lib.lib().pnfx_flash_fwd(
         *_ptr4(q), *_ptr4(k), *_ptr4(v), *_ptr4(o), o_lo.data_ptr() if bf else None,
@@ -334,6 +346,8 @@ def flash_bwd(q: Tensor, k: Tensor, v: Tensor, tau: Tensor, o: Tensor, o_lo: Ten
     dk = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
     dv = torch.empty((B, H, N, D), device=q.device, dtype=q.dtype)
     dtau = torch.empty(1, device=q.device, dtype=torch.float32)
+    if B * H * N == 0:  # empty input: empty gradients, dtau = -(sum over no scores) = 0
+        return dq, dk, dv, dtau.zero_()
     L = _lib.lib()
     ws_bytes = L.pnfx_flash_bwd_workspace_size(B, H, N, D)
     ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
