@@ -494,6 +494,47 @@ def test_flash_full_size_slice_matches_oracle(dev, name, B, H, N, D, std, tau, s
     assert_bf16_close(to_np64(Z[b, h]), Zo, f"{name} Z")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_flash_longest_sequence_rows_match_oracle(dev, D):
+    """The longest sequence with a tile mask (and, at d = 64, the silent-tile bound):
+    N = 65536, 1024 key tiles.  Rows of O, M, Z and dQ, and the last eight keys' dK and dV,
+    against the float64 oracle.  Causal row i of the oracle is the non-causal problem of query i over
+    keys 0..i, so each checked row is one small oracle call; the last eight keys' gradients
+    are the sums of the last eight rows' contributions.  Every third of the first 128 key
+    blocks is zeroed and tau > 0, so the forward's tile list and the gradient kernels'
+    silent sub-tiles are exercised at this size."""
+    print(f"[flash N=65536 rows D={D}]", flush=True)
+    B, H, N, tau = 1, 1, 65536, 0.1
+    g = torch.Generator().manual_seed(17)
+    std = (64 / D) ** 0.25  # scores of the same spread at both head dims
+    q, k, v, dO = [(torch.randn(B, H, N, D, generator=g) * std).to(torch.bfloat16).to(dev)
+                   for _ in range(4)]
+    for j in range(0, 128, 3):
+        k[:, :, 64 * j:64 * j + 64] = 0
+    o, dq, dk, dv, _ = _run(q, k, v, tau, dO, None, 0.5, True)
+    _, M, Z, _, _ = flash_pn_fir_tau_attention_with_stats(q, k, v, torch.tensor(tau, device=dev))
+    qn, kn, vn, dn = (to_np64(t[0, 0]) for t in (q, k, v, dO))
+    scale = 1.0 / np.sqrt(D)
+    rows = [0, 1, 63, 64, 200, 4095, 32768] + list(range(N - 8, N))
+    Of, Mo, Zo, rq = [], [], [], []
+    rk, rv = np.zeros((8, D)), np.zeros((8, D))
+    for i in rows:
+        oi, mi, zi, _ = O.flash_fwd(qn[i:i + 1], kn[:i + 1], vn[:i + 1], tau, scale, 0.5, False)
+        dqi, dki, dvi, _ = O.flash_bwd(qn[i:i + 1], kn[:i + 1], vn[:i + 1], tau, dn[i:i + 1],
+                                       scale, 0.5, False)
+        Of.append(oi[0]), Mo.append(mi[0]), Zo.append(zi[0]), rq.append(dqi[0])
+        if i >= N - 8:  # row i reaches keys N - 8 .. i
+            rk[:i + 1 - (N - 8)] += dki[N - 8:]
+            rv[:i + 1 - (N - 8)] += dvi[N - 8:]
+    pick = lambda t: to_np64(t[0, 0])[rows]  # noqa: E731
+    assert_bf16_close(pick(o), np.array(Of), "N=65536 O rows")
+    assert_close(pick(M), np.array(Mo), 1e-5, 1e-5, "N=65536 M rows")
+    assert_bf16_close(pick(Z), np.array(Zo), "N=65536 Z rows")
+    assert_bf16_close(pick(dq), np.array(rq), "N=65536 dQ rows")
+    assert_bf16_close(to_np64(dk[0, 0])[N - 8:], rk, "N=65536 dK last keys")
+    assert_bf16_close(to_np64(dv[0, 0])[N - 8:], rv, "N=65536 dV last keys")
+
+
 def test_flash_full_size_gradients_scale_exactly_with_dout(dev):
     """Size-independent property at C4: the backward is linear in dO and every operation in
     it commutes with a power-of-two scale, so doubling dO doubles dQ, dK, dV and dtau
