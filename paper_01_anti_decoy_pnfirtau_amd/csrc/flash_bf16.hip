@@ -836,58 +836,50 @@ __device__ __forceinline__ float pow9_unit(float s) {
   return (t2 * t2) * s;
 }
 
-// dS/(10 scale x 2^9e) for the 16 scores a lane holds in one 32-key half tile of the dQ
-// kernel (S^T layout, one query row per lane, scores scaled by 2^-e), written over
-// dw = dW - D: u^9 dw + [u == M] G'' (u, M, G'' in the scaled units).
-// COUNT also counts the peak ties per query block.
-template <bool COUNT, int QB>
+// dS/(10 scale x 2^9e) for the 8 scores a lane holds in query block qb of one 32-key half
+// tile of the dQ kernel (S^T layout, one query row per lane, scores scaled by 2^-e), written
+// over dw = dW - D: u^9 dw + [u == M] G'' (u, M, G'' in the scaled units).  Also counts the
+// row's peak ties.
+template <int QB>
 __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB], int (&cnt)[QB],
-                                      const float (&rM)[QB], const float (&rG)[QB]) {
+                                      const float (&rM)[QB], const float (&rG)[QB], int qb) {
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
+  for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float u9 = pow9_unit(s[kk][qb][i]);
-        const bool tie = s[kk][qb][i] == rM[qb];  // M > 0; G'' = 0 on silent rows
-        dw[kk][qb][i] = __builtin_fmaf(u9, dw[kk][qb][i], tie ? rG[qb] : 0.f);
-        if (COUNT) cnt[qb] += tie ? 1 : 0;
-      }
+    for (int i = 0; i < 4; ++i) {
+      const float u9 = pow9_unit(s[kk][qb][i]);
+      const bool tie = s[kk][qb][i] == rM[qb];  // M > 0; G'' = 0 on silent rows
+      dw[kk][qb][i] = __builtin_fmaf(u9, dw[kk][qb][i], tie ? rG[qb] : 0.f);
+      cnt[qb] += tie ? 1 : 0;
+    }
 }
 
-// ds_kq without the peak-tie term, for half tiles where no row of the wave has a key at its
-// peak: dS/(10 scale x 2^9e) = u^9 (dW - D).
+// ds_kq without the peak-tie term, for a query block where no row of the wave has a key of
+// the half tile at its peak: dS/(10 scale x 2^9e) = u^9 (dW - D).
 template <int QB>
-__device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB]) {
+__device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB], int qb) {
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
+  for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dw[kk][qb][i] = pow9_unit(s[kk][qb][i]) * dw[kk][qb][i];
+    for (int i = 0; i < 4; ++i) dw[kk][qb][i] = pow9_unit(s[kk][qb][i]) * dw[kk][qb][i];
 }
 
-// Whether some lane of the wave holds a score tied at its row's peak M on a row whose tie
-// term is non-zero.  Every score is <= M (M is the forward's maximum of the same MFMA
-// values), so a tie is a lane maximum equal to M; the maximum is an integer max over the raw
-// bit patterns (order-preserving for positive floats; negatives, and the mask's -1, stay
-// below any M > 0).  Half a VALU op per score against three for the tie compare, select and
-// count of ds_kq.
+// Whether some lane of the wave holds, in query block qb, a score tied at its row's peak M on
+// a row whose tie term is non-zero.  Every score is <= M (M is the forward's maximum of the
+// same MFMA values), so a tie is a lane maximum equal to M; the maximum is an integer max
+// over the raw bit patterns (order-preserving for positive floats; negatives, and the mask's
+// -1, stay below any M > 0).  Half a VALU op per score against three for the tie compare,
+// select and count of ds_kq.  Taken per 16-row block, the tie path runs on about half as
+// many blocks as it would per 32-row half tile.
 template <int QB>
-__device__ __forceinline__ bool any_peak_tie(const f32x4 (&s)[2][QB], const float (&rM)[QB],
-                                             const float (&rG)[QB]) {
-  bool t = false;
+__device__ __forceinline__ bool peak_tie(const f32x4 (&s)[2][QB], const float (&rM)[QB],
+                                         const float (&rG)[QB], int qb) {
+  int mx = f2i(s[0][qb][0]);
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    int mx = f2i(s[0][qb][0]);
+  for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) mx = max(mx, f2i(s[kk][qb][i]));
-    t = t || (mx >= f2i(rM[qb]) && rG[qb] != 0.f);
-  }
-  return __any(t);
+    for (int i = 0; i < 4; ++i) mx = max(mx, f2i(s[kk][qb][i]));
+  return __any(mx >= f2i(rM[qb]) && rG[qb] != 0.f);
 }
 
 // dQ: query-parallel, same tiling as the forward (4 waves x 32 rows, 64-key tiles), K and V
@@ -1105,11 +1097,14 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
         }
         affine_kq_rows<PS>(s, sc_e, nt_e);
         if (masked) mask_kq(s, n0, hf, qrow0, N, CAUSAL, g, r16);
-        if (any_peak_tie(s, rM, rG)) {
-          ds_kq<true>(s, dw, cnt, rM, rG);
-          code |= 2 << hf;
-        } else {
-          ds_kq_notie(s, dw);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          if (peak_tie(s, rM, rG, qb)) {
+            ds_kq(s, dw, cnt, rM, rG, qb);
+            code |= 2 << hf;
+          } else {
+            ds_kq_notie(s, dw, qb);
+          }
         }
         bf16x8 pf[QB];
 #pragma unroll
