@@ -226,6 +226,18 @@ int pnfx_flash_bwd_noalloc(const void* q, int64_t qsb, int64_t qsh, int64_t qsn,
                            float scale, float gamma, int has_gamma, int causal, int dtype,
                            void* stream);
 
+/*
+ * Diagnostic, not on the attention path; no counterpart in the reference.  Times a
+ * register-only loop of mfma_per_iter independent bf16 MFMAs (16x16x32, or half as many
+ * 32x32x16 when mfma_32x32) and valu_per_iter independent fp32 FMAs, iters times, on one
+ * workgroup per CU at waves_per_simd (1 or 2) waves per SIMD: ms[0] with the MFMAs only,
+ * ms[1] with the FMAs only, ms[2] with both.  (mfma_per_iter, valu_per_iter) is one of
+ * (8, 32), (8, 64), (16, 64).  out: device scratch of 256 * 512 floats.  Blocks until the
+ * launches on stream finish.
+ */
+int pnfx_probe_pipe_overlap(int waves_per_simd, int mfma_32x32, int mfma_per_iter,
+                            int valu_per_iter, int iters, float* out, float* ms, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@ def _declare(lib: ctypes.CDLL) -> None:
             + [vp, vp, vp, vp, i64, i64, i64, i64, vp, f32, f32, i32, i32, vp, i64, i32, i32, vp],
             i32),
         "pnfx_flash_fwd_workspace_size": ([i64, i64, i64, i64], i64),
+        "pnfx_probe_pipe_overlap": ([i32, i32, i32, i32, i32, vp, vp, vp], i32),
         "pnfx_flash_bwd_workspace_size": ([i64, i64, i64, i64], i64),
         "pnfx_flash_bwd": (
             [vp, i64, i64, i64] * 4
@@ -92,5 +93,5 @@ def exported_symbols() -> list[str]:
         "pnfx_pn_rows_fwd", "pnfx_pn_rows_bwd", "pnfx_flash_fwd", "pnfx_flash_fwd_fir",
         "pnfx_flash_fwd_workspace_size",
         "pnfx_flash_bwd_workspace_size", "pnfx_flash_bwd", "pnfx_flash_bwd_stages",
-        "pnfx_flash_bwd_noalloc",
+        "pnfx_flash_bwd_noalloc", "pnfx_probe_pipe_overlap",
     ]
