@@ -3,7 +3,8 @@
  *
  * Every entry point takes device pointers, element strides and sizes, and a
  * hipStream_t passed as `void*` (NULL = the legacy default stream).  Kernels are
- * enqueued on that stream; nothing blocks the host and nothing is allocated:
+ * enqueued on that stream; nothing blocks the host (the diagnostic
+ * pnfx_probe_pipe_overlap aside) and nothing is allocated:
  * callers own every buffer, including the workspace of pnfx_flash_bwd (the one
  * exception, pnfx_flash_bwd_noalloc, uses a scratch array the library holds).
  *
