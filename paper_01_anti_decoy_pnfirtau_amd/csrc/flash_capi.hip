@@ -16,7 +16,8 @@ namespace {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Each [B, H, N, D] operand must have unit inner stride; the bf16 MFMA kernels read and
-// write whole 16-byte (8-element) chunks of a row.
+// write whole 16-byte (8-element) chunks of a row, and their tile loads address the rows of a
+// 64-row tile by 32-bit byte offsets from the tile's first row (2 * 63 * sn < 2^32).
 int check_operand(const char* name, const void* p, int64_t sb, int64_t sh, int64_t sn, int dtype) {
   PNFX_REQUIRE(p != nullptr, "flash: %s is null", name);
   if (dtype == PNFX_BF16) {
@@ -24,6 +25,8 @@ int check_operand(const char* name, const void* p, int64_t sb, int64_t sh, int64
                  "flash: %s must be 16-byte aligned with strides that are multiples of 8 "
                  "elements (got %lld, %lld, %lld)",
                  name, (long long)sb, (long long)sh, (long long)sn);
+    PNFX_REQUIRE(sn >= 0 && sn < (1ll << 25), "flash: %s row stride %lld outside [0, 2^25)",
+                 name, (long long)sn);
   }
   return PNFX_OK;
 }

@@ -131,6 +131,12 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     rc = lib.pnfx_flash_fwd(*([None, 0, 0, 0] * 4), None, None, None, None, None, None, 0,
                             1, 1, 8, 48, None, 0.125, 0.5, 1, 1, 1, None)
     assert rc == -1 and b"head dim" in lib.pnfx_last_error()
+    # a bf16 row stride the tile loads' 32-bit row offsets cannot span
+    fake16 = ctypes.c_void_p(256)
+    ok = [fake16, 64 * 8, 64 * 8, 64]
+    rc = lib.pnfx_flash_fwd(*ok, fake16, 64 * 8, 64 * 8, 1 << 25, *ok, *ok, None, fake16, fake16,
+                            None, None, None, 0, 1, 1, 8, 64, fake16, 0.125, 0.5, 1, 1, 1, None)
+    assert rc == -1 and b"k row stride" in lib.pnfx_last_error()
     rc = lib.pnfx_fir_fwd(None, 0, 0, 0, None, 1, 1, 4, 8, None, 1, 7, 1, None)
     assert rc == -1 and b"null" in lib.pnfx_last_error()
     rc = lib.pnfx_fir_fwd(ctypes.c_void_p(16), 0, 0, 0, ctypes.c_void_p(16), 1, 1, 4, 8,
