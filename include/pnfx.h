@@ -98,7 +98,8 @@ int pnfx_pn_rows_bwd(const void* dw, int64_t dw_rs, const void* raw, int64_t raw
 
 /*
  * Flash pn_fir_tau attention forward (p = 10, peak gate), O(N) memory.
- *   q, k, v, o : [B, H, N, D] with strides (s?b, s?h, s?n, 1), same dtype
+ *   q, k, v, o : [B, H, N, D] with strides (s?b, s?h, s?n, 1), same dtype; bf16:
+ *                16-byte aligned, strides multiples of 8, row strides s?n < 2^25
  *   o_lo       : optional (may be NULL; bf16 only), o's strides: the bf16 rounding
  *                residual of O (fp32 O = o + o_lo to ~16 mantissa bits), which
  *                pnfx_flash_bwd uses to form D = <dO, O>/gate accurately
