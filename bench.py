@@ -46,6 +46,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 METRIC = "pn_fir_tau flash fwd+bwd TFLOP/s (%MFMA peak) N=8192 d64 bf16; FIR GB/s"
@@ -93,19 +94,36 @@ def silent_tile_stats(q, k, v, tau):
             "silent_fraction_nb2_convention": round(1 - active / (nb * nb * m64.shape[0]), 4)}
 
 
-def time_steps(step, steps, warmup):
+def time_steps_detail(step, steps, warmup):
+    """W untimed warm-up steps, then K timed steps between two synchronisations.  Returns
+    (wall ms per step, event ms per step, the K per-step event durations): an event is
+    recorded on the stream before every step and after the last (no synchronisation
+    inside the timed region)."""
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(steps):
+    for i in range(steps):
+        evs[i].record()
         step()
-    ev1.record()
+    evs[steps].record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps * 1e3
-    return wall, ev0.elapsed_time(ev1) / steps
+    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
+    return wall, evs[0].elapsed_time(evs[steps]) / steps, per
+
+
+def time_steps(step, steps, warmup):
+    wall, ev, _ = time_steps_detail(step, steps, warmup)
+    return wall, ev
+
+
+def spread(per):
+    """Median and interquartile range (ms) of per-step durations."""
+    a = np.sort(np.asarray(per, dtype=np.float64))
+    q1, med, q3 = np.percentile(a, [25, 50, 75])
+    return {"median": round(float(med), 4), "iqr": [round(float(q1), 4), round(float(q3), 4)]}
 
 
 def flash_step_fn(q, k, v, dO, tau_val):
@@ -684,7 +702,7 @@ def main():
     if args.only != "flash":
         kern = kernel_times(q, k, v, dO, 0.0, max(5, args.steps // 2))
     step = flash_step_fn(q, k, v, dO, 0.0)
-    wall_ms, ev_ms = time_steps(step, args.steps, args.warmup)
+    wall_ms, ev_ms, per_ms = time_steps_detail(step, args.steps, args.warmup)
     if args.only == "flash":
         print(json.dumps({"ms_per_step": wall_ms, "event_ms": ev_ms}))
         return
@@ -696,7 +714,7 @@ def main():
     frac = plant_silent(ks, N)
     tile_stats = silent_tile_stats(q, ks, v, 0.25)
     step_s = flash_step_fn(q, ks, v, dO, 0.25)
-    wall_s, ev_s = time_steps(step_s, args.steps, args.warmup)
+    wall_s, ev_s, per_s = time_steps_detail(step_s, args.steps, args.warmup)
     del step_s, ks
 
     fir = bench_fir(dev)
@@ -708,7 +726,8 @@ def main():
     # and warm-up as C4: the FIR and copy timings before this leave the GPU at a lower clock
     kernel_times(q5, k5, v5, dO5, 0.0, max(3, args.steps // 4))
     kern5 = kernel_times(q5, k5, v5, dO5, 0.0, max(3, args.steps // 4))
-    wall5, ev5 = time_steps(flash_step_fn(q5, k5, v5, dO5, 0.0), args.steps, args.warmup)
+    wall5, ev5, per5 = time_steps_detail(flash_step_fn(q5, k5, v5, dO5, 0.0), args.steps,
+                                         args.warmup)
     flops5 = 7 * gemm_flops(B5, H5, N5, D5)
     del q5, k5, v5, dO5
 
@@ -746,6 +765,7 @@ def main():
                    "silent_tile_fraction": 0.0, "alg_tflop_per_step": round(flops / 1e12, 4)},
         "frac_mfma_peak": round(value / PEAK_BF16_TFLOPS, 4),
         "event_ms_per_step": round(ev_ms, 4),
+        "step_event_ms": spread(per_ms),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved,
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": profiled_traffic(dom),
@@ -753,9 +773,10 @@ def main():
         "kernels": kern,
         "silent_50": {"silent_fraction": round(frac, 4), "tau": 0.25, **tile_stats,
                       "ms_per_step": round(wall_s, 4), "event_ms_per_step": round(ev_s, 4),
-                      "speedup": round(wall_ms / wall_s, 3)},
+                      "step_event_ms": spread(per_s), "speedup": round(wall_ms / wall_s, 3)},
         "fir": fir,
         "wide_head": {"config": C5, "ms_per_step": round(wall5, 4),
+                      "step_event_ms": spread(per5),
                       "tflops": round(flops5 / (wall5 * 1e-3) / 1e12, 2),
                       "kernel_ms": {n: r["ms"] for n, r in kern5.items()}},
         "flash_fp32": {"config": F32, "ms_per_step": round(wallf, 4),
