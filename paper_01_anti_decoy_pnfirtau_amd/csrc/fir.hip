@@ -3,18 +3,23 @@
 // Streaming, HBM-bound.  Each thread owns one 16-byte channel chunk of RUN = 8 consecutive
 // sequence rows of one (b, h) slice: it issues all RUN + K - 1 row loads up front (the
 // K - 1 row causal halo is served by L2: the neighbouring run of the same wave reads those
-// rows at the same time), evaluates the fp32 fused multiply-add chain in lag order and
-// writes RUN 16-byte rows with non-temporal stores (the output is streamed, not re-read by
-// this kernel).  Eight consecutive lanes cover one 128-byte row of a d = 64 bf16 head, so
+// rows at the same time), evaluates the fp32 fused multiply-add chains in lag order, one
+// input row at a time (each row widened to fp32 once and fed to every output that uses it),
+// and writes RUN 16-byte rows with non-temporal stores (the output is streamed, not re-read
+// by this kernel).  Eight consecutive lanes cover one 128-byte row of a d = 64 bf16 head, so
 // every load and store instruction moves whole cache lines.  Of the variants measured on
-// MI355X (runs of 2..64 rows, an LDS-staged 64-row tile, non-temporal loads), this one is
-// the fastest; on the 32 MiB benchmark tensor it takes about 1.15x the time of the runtime's
-// device copy of the same bytes (the extra time is the tap arithmetic, ~9 VALU operations per
-// output element, and the re-read causal halo).
+// MI355X (runs of 2..64 rows, an LDS-staged 64-row tile, non-temporal loads, stores issued as
+// soon as each output is complete), this one is the fastest; on the 32 MiB benchmark tensor
+// it takes about 0.96x the time of the runtime's device copy of the same bytes.  At that size
+// every workgroup is resident at once, so the arithmetic (about 9.5 VALU operations per
+// output element, 7 of them the FMA chain) lies between the loads and the stores: widening
+// every input element once per use instead of once per row took 1.2x as long.
 //
 // Numerics follow src/triton_pnfirtau.py:72-84 (forward) and :120-132 (adjoint):
 // acc = x[n] * h0; acc = fma(x[n -/+ u], h_u, acc) for u = 1..K-1 while in range;
 // h_u = taps[K-1-u] in fp32; one rounding to the storage type at the store.
+#include <type_traits>
+
 #include "pnfx_common.h"
 
 namespace pnfx {
@@ -98,8 +103,11 @@ __global__ __launch_bounds__(256) void fir_vec_kernel(FirArgs a) {
   // Window row w holds sequence row m = base + w.
   const int base = ADJ ? n0 : n0 - (KT - 1);
   u32x4 win[WIN];
+  // Loads in the order the chain below uses the rows (loads complete in order, so the first
+  // terms can start while the rest are in flight).
 #pragma unroll
-  for (int w = 0; w < WIN; ++w) {
+  for (int i = 0; i < WIN; ++i) {
+    const int w = ADJ ? i : WIN - 1 - i;
     const int m = base + w;
     if (m >= 0 && m < N) {
       win[w] = *reinterpret_cast<const u32x4*>(xs + (int64_t)m * a.sn);
@@ -108,27 +116,46 @@ __global__ __launch_bounds__(256) void fir_vec_kernel(FirArgs a) {
     }
   }
   T* ys = reinterpret_cast<T*>(a.y) + ((int64_t)bh * N + n0) * a.C + ch * VEC;
+  // Window rows in the order of increasing lag (newest first for the forward, oldest first
+  // for the adjoint): each row is widened to fp32 once and feeds every output of the run
+  // that uses it, as that output's next term.  Output j (row n = n0 + j) sits at window
+  // index w0 = j + KT - 1 (forward) or j (adjoint) and takes lag u from window row w0 -/+ u,
+  // so it still sees its terms in lag order u = 0, 1, ..., K - 1: the same chain and the same
+  // roundings as one output at a time, with the widening done once per row instead of once
+  // per use.
+  float acc[RUN][VEC];
+  // Away from the sequence ends every lag of every output of the run is in range; only runs
+  // within K - 1 rows of an end take the per-term range test (wave-uniform in practice).
+  const bool interior = ADJ ? (n0 + RUN + KT - 2 < N) : (n0 >= KT - 1);
+  const auto chain = [&](auto checked) {
 #pragma unroll
-  for (int j = 0; j < RUN; ++j) {
-    const int n = n0 + j;
-    if (n < N) {
-      float acc[VEC];
-      const int w0 = ADJ ? j : j + KT - 1;  // window index of row n
+    for (int i = 0; i < WIN; ++i) {
+      const int w = ADJ ? i : WIN - 1 - i;
+      float xe[VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] = chunk_elem<T>(win[w0], e) * h[0];
+      for (int e = 0; e < VEC; ++e) xe[e] = chunk_elem<T>(win[w], e);
 #pragma unroll
-      for (int u = 1; u < KT; ++u) {
-        const bool ok = (u < K) && (ADJ ? (n + u < N) : (n - u >= 0));
-        if (ok) {
-          const int wu = ADJ ? w0 + u : w0 - u;
+      for (int j = 0; j < RUN; ++j) {
+        const int w0 = ADJ ? j : j + KT - 1;
+        const int u = ADJ ? w - w0 : w0 - w;  // lag of window row w for output j
+        if (u < 0 || u >= KT) continue;       // compile-time after unrolling
+        const int n = n0 + j;
+        if (u == 0) {
 #pragma unroll
-          for (int e = 0; e < VEC; ++e)
-            acc[e] = __builtin_fmaf(chunk_elem<T>(win[wu], e), h[u], acc[e]);
+          for (int e = 0; e < VEC; ++e) acc[j][e] = xe[e] * h[0];
+        } else if ((KT == 7 || u < K) &&
+                   (!decltype(checked)::value || (ADJ ? (n + u < N) : (n - u >= 0)))) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[j][e] = __builtin_fmaf(xe[e], h[u], acc[j][e]);
         }
       }
-      store_chunk<T>(ys + (int64_t)j * a.C, acc);
     }
-  }
+  };
+  if (interior) chain(std::integral_constant<bool, false>{});
+  else chain(std::integral_constant<bool, true>{});
+#pragma unroll
+  for (int j = 0; j < RUN; ++j)
+    if (n0 + j < N) store_chunk<T>(ys + (int64_t)j * a.C, acc[j]);
 }
 
 // One thread per output element; any channel stride / alignment.
