@@ -571,3 +571,62 @@ def test_flash_full_size_planted_tile_mask(dev):
     act, amb = O.tile_activity(to_np64(q[1, 7]), to_np64(k[1, 7]), 0.25)
     assert not amb.any()
     assert np.array_equal(m64[1, 7], act)
+
+
+def _random_cases(n, seed=20261202):
+    """n seeded draws of (B, H, N, D, tau, gamma, causal, scale, std, packed, dtype): shapes
+    off the tile grid, every head size, negative / zero / positive tau, gamma None, both
+    mask modes, scales that are and are not powers of two, input scales 0.5-2 and q/k/v as
+    strided views of one packed [B, N, 3, H, D] tensor (the MHA modules' layout)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        D = int(rng.choice([16, 32, 64, 128]))
+        N = int(rng.integers(2, 700))
+        tau = float(rng.choice([0.0, round(float(rng.uniform(-0.3, 0.4)), 3)]))
+        gamma = [0.5, None, 0.25][int(rng.integers(0, 3))]
+        causal = bool(rng.random() < 0.7)
+        scale = float(rng.choice([D ** -0.5, round(float(rng.uniform(0.05, 0.3)), 4)]))
+        std = float(rng.choice([0.5, 1.0, 2.0]))
+        packed = bool(rng.random() < 0.5)
+        dtype = torch.float32 if i % 4 == 3 else torch.bfloat16
+        out.append((int(rng.integers(1, 3)), int(rng.integers(1, 4)), N, D, tau, gamma, causal,
+                    scale, std, packed, dtype))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_cases(16))
+def test_flash_random_shapes_match_oracle(dev, case):
+    """Seeded sweep beyond the fixed cases: O, dQ, dK, dV and dtau against the float64
+    oracle, at the same bars (bf16 elementwise rtol 2e-2 / atol 2e-3 of the tensor's scale,
+    or 1.25x the reference's own rounding; fp32 1e-5)."""
+    B, H, N, D, tau, gamma, causal, scale, std, packed, dtype = case
+    print(f"[flash random B={B} H={H} N={N} D={D} tau={tau} gamma={gamma} causal={causal} "
+          f"scale={scale:.4f} std={std} packed={packed} {dtype}]", flush=True)
+    seed = (N * 131 + D * 7 + H) % 10007
+    dO = seeded((B, H, N, D), seed + 3, dtype, dev)
+    if packed:
+        # q, k, v as the [B, H, N, D] strided views of one packed tensor, passed as they are;
+        # the gradients land in the packed tensor's grad
+        qkv = seeded((B, N, 3, H, D), seed, dtype, dev, std).requires_grad_(True)
+        q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+        assert not q.is_contiguous()
+        t = torch.tensor(tau, device=dev, requires_grad=True)
+        o = flash_pn_fir_tau_attention(q, k, v, t, scale=scale, gamma=gamma, causal_mask=causal)
+        o.backward(dO)
+        torch.cuda.synchronize()
+        dq, dk, dv = (qkv.grad[:, :, i].transpose(1, 2) for i in range(3))
+        dtau = t.grad
+        q, k, v = (x.detach().contiguous() for x in (q, k, v))
+    else:
+        q, k, v = (seeded((B, H, N, D), seed + i, dtype, dev, std) for i in range(3))
+        o, dq, dk, dv, dtau = _run(q, k, v, tau, dO, scale, gamma, causal)
+    Of, M, Z, Nm, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, tau, dO, scale, gamma, causal)
+    em = flash_reference_rounding(q, k, v, tau, dO, scale, gamma, causal)
+    for name, got, want in (("O", o, Of), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        if dtype == torch.bfloat16:
+            assert_bf16_close(to_np64(got), want, name, em.get(name))
+        else:
+            assert_close(to_np64(got), want, F32_TOL, F32_TOL, name)
+    tol = BF16_ATOL if dtype == torch.bfloat16 else F32_TOL
+    assert_sum_close(float(dtau), rdt, dabs, tol, "dtau")
