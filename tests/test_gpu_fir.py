@@ -84,3 +84,17 @@ def test_fir_autograd_is_the_adjoint(dev):
     lhs = float((y.double() * g.double()).sum())
     rhs = float((x.detach().double() * x.grad.double()).sum())
     assert abs(lhs - rhs) < 1e-4 * max(1.0, abs(lhs))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N", [1, 6, 9, 37, 130])
+def test_fir_adjoint_short_and_ragged_sequences_bit_exact(dev, dtype, N):
+    """The 7-tap adjoint where runs of 8 rows straddle both ends of the sequence (the kernel's
+    range-tested path) as well as the interior."""
+    print(f"[fir adjoint N={N} {dtype}]", flush=True)
+    x = seeded((2, 3, N, 64), 9, dtype, dev)
+    taps = _per_head_taps(3, 7, 11).to(dev)
+    gy = torch.ops.pnfx.fir_bwd(x, taps)
+    ref = _oracle_bhnc(x.cpu().reshape(6, N, 64), taps.cpu().repeat(2, 1), True)
+    got = bf16_bits(gy) if dtype == torch.bfloat16 else gy.cpu().numpy()
+    assert np.array_equal(got.reshape(6, N, 64), ref)
