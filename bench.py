@@ -15,7 +15,8 @@ Also measured in the same run and reported on the same JSON line:
   silent (zero key blocks {even j} \\ {96}, tau = 0.25) and the speedup;
 * ``fir``: standalone causal FIR (config C2, K [8,8,2048,64] bf16, per-head
   taps) in GB/s, rotating 20 input/output buffer pairs (640 MiB) so the 256 MB
-  Infinity Cache cannot serve repeats;
+  Infinity Cache cannot serve repeats, beside a device copy of the same bytes and the
+  FIR's adjoint (the key gradient);
 * ``wide_head``: config C5 (B=8, H=8, N=4096, d=128) TFLOP/s;
 * ``flash_fp32``: the fp32 flash path (B=1, H=8, N=2048, d=64), ms per fwd+bwd step;
 * ``fir_fused_forward``: C4 forward from raw keys, FIR + flash forward against the forward
@@ -205,33 +206,38 @@ def bench_fir(dev, reps=200, pairs=20, B=8):
     from paper_01_anti_decoy_pnfirtau_amd import _lib
 
     L = _lib.lib()
-
-    def launch(i):
-        x, y = xs[i % pairs], ys[i % pairs]
-        st = torch.cuda.current_stream().cuda_stream
-        rc = L.pnfx_fir_fwd(x.data_ptr(), x.stride(0), x.stride(1), x.stride(2), y.data_ptr(),
-                            B, 8, 2048, 64, taps.data_ptr(), 8, 7, _lib.PNFX_BF16, st)
-        _lib.check(rc, "pnfx_fir_fwd")
-
-    for i in range(pairs):
-        launch(i)
-    torch.cuda.synchronize()
-    # One launch per buffer pair, captured in a HIP graph so that host launch latency does
-    # not leave the GPU idle between these few-microsecond kernels.
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(pairs):
-            launch(i)
-    graph.replay()
-    torch.cuda.synchronize()
     rounds = max(1, reps // pairs)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(rounds):
+
+    def timed(entry):
+        def launch(i):
+            x, y = xs[i % pairs], ys[i % pairs]
+            st = torch.cuda.current_stream().cuda_stream
+            rc = getattr(L, entry)(x.data_ptr(), x.stride(0), x.stride(1), x.stride(2),
+                                   y.data_ptr(), B, 8, 2048, 64, taps.data_ptr(), 8, 7,
+                                   _lib.PNFX_BF16, st)
+            _lib.check(rc, entry)
+
+        for i in range(pairs):
+            launch(i)
+        torch.cuda.synchronize()
+        # One launch per buffer pair, captured in a HIP graph so that host launch latency does
+        # not leave the GPU idle between these few-microsecond kernels.
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(pairs):
+                launch(i)
         graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) / (rounds * pairs) * 1e3
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(rounds):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (rounds * pairs) * 1e3
+
+    us = timed("pnfx_fir_fwd")
+    us_adj = timed("pnfx_fir_bwd")  # the adjoint (the key gradient), same bytes
     nbytes = 2 * B * 8 * 2048 * 64 * 2
     gbps = nbytes / (us * 1e-6) / 1e9
     # reference point: a plain device copy of the same bytes over the same buffers
@@ -251,7 +257,9 @@ def bench_fir(dev, reps=200, pairs=20, B=8):
             "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
             "buffers": f"{pairs} pairs x {nbytes >> 20} MiB",
             "same_bytes_copy_us": round(cus, 3),
-            "same_bytes_copy_gbps": round(nbytes / (cus * 1e-6) / 1e9, 1)}
+            "same_bytes_copy_gbps": round(nbytes / (cus * 1e-6) / 1e9, 1),
+            "adjoint_us_per_launch": round(us_adj, 3),
+            "adjoint_gbps": round(nbytes / (us_adj * 1e-6) / 1e9, 1)}
 
 
 def bench_fir_sweep(dev):
