@@ -753,7 +753,8 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
 // The bf16 row constants are eight planes of N floats per (b, h): M, -D, G'', x, rho, kappa,
 // -kappa D, and G/Nmax (written by the dQ kernel, which counts the ties).  For D <= 64 the
 // dK/dV kernel forms its scores scaled by 2^-e per row (see pow9_unit), and planes 4, 5 hold
-// M 2^-e and -tau 2^-e instead of rho and kappa; plane 7 then holds G'' 2^-9e / Nmax.
+// M 2^-e and -tau 2^-e instead of rho and kappa, plane 6 is not written (nor rho, a powf,
+// computed), and plane 7 holds G'' 2^-9e / Nmax.
 // Exponent e of a row peak, M = m 2^e with m in [0.5, 1) (0 for silent rows), kept within
 // +-64: a peak below 2^-64 then scales to below 1 all the same, and one above 2^64 has already
 // overflowed the forward's u^10.
@@ -805,22 +806,22 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
     const float Dv = g > 0.f ? dot / g : 0.f;
     float dgate = 0.f;
     if (HAS_GAMMA && M > 0.f) dgate = p.gamma / ((M + p.gamma) * (M + p.gamma));
-    const float rho = powf(x, 0.1f);
-    const float kappa = 10.f * p.scale * rho;
     const int64_t bh = row / p.N, i = row % p.N;
     rc_plane(p, bh, 0)[i] = M;
     rc_plane(p, bh, 1)[i] = -Dv;
     rc_plane(p, bh, 2)[i] = x > 0.f ? Dv * dgate / (10.f * x) : 0.f;
     rc_plane(p, bh, 3)[i] = x;
-    if (D <= 64) {  // the peak-normalised scores of the dK/dV kernel
+    if (D <= 64) {  // the peak-normalised scores of the dK/dV kernel (plane 6 unused)
       const int e = peak_exponent(M);
       rc_plane(p, bh, 4)[i] = __builtin_amdgcn_ldexpf(M, -e);
       rc_plane(p, bh, 5)[i] = __builtin_amdgcn_ldexpf(-p.tau[0], -e);
-    } else {
+    } else {  // the a = rho u form of the D = 128 dK/dV kernel
+      const float rho = powf(x, 0.1f);
+      const float kappa = 10.f * p.scale * rho;
       rc_plane(p, bh, 4)[i] = rho;
       rc_plane(p, bh, 5)[i] = kappa;
+      rc_plane(p, bh, 6)[i] = -kappa * Dv;
     }
-    rc_plane(p, bh, 6)[i] = -kappa * Dv;
   }
 }
 
