@@ -211,6 +211,47 @@ def test_flash_stats_and_planted_ties(dev, dtype, scale):
     assert_sum_close(float(dtau), rdt, dabs, tol, "dtau")
 
 
+def test_flash_ties_in_alternate_row_quads(dev):
+    """Peak ties on some rows of a 32-row group only: in rows 160-191 the rows r with bit 2 of
+    r - 160 set (164-167, 172-175, ...) peak on a triplicated key, in rows 192-223 those with
+    bit 2 clear peak on a duplicated one.  The backward locates peak ties per block of rows
+    and keys (the dQ stage's 16-row blocks, the dK/dV stage's 32-row halves, whose rows the
+    MFMA layouts split into these alternating quads), so a tie attributed to the wrong block
+    drops its gradient from dK.
+    The tied keys carry duplicated values and the planted rows peak near gamma with a large
+    dO, so the tie term dominates those rows' gradient: dropping it from the float64 oracle for
+    the 8 rows of any one 16-row block, or for all 16 of a group, puts dK at the tied keys
+    27-178 times past the elementwise tolerance, where the reference kernels' own bf16
+    rounding reaches 5.6 (checked on the CPU)."""
+    B, H, N, D = 1, 2, 256, 64
+    dtype, scale = torch.bfloat16, 1 / 8
+    q = seeded((B, H, N, D), 40, dtype, dev)
+    k = seeded((B, H, N, D), 41, dtype, dev)
+    v = seeded((B, H, N, D), 42, dtype, dev)
+    dO = seeded((B, H, N, D), 43, dtype, dev)
+    for dup, src in ((100, 40), (150, 40), (130, 60)):
+        k[:, :, dup] = k[:, :, src]
+        v[:, :, dup] = v[:, :, src]
+    rows_a = [r for r in range(160, 192) if (r - 160) & 4]
+    rows_b = [r for r in range(192, 224) if not (r - 192) & 4]
+    for rows, key in ((rows_a, 40), (rows_b, 60)):
+        # the peak score q.k scale lands at 0.5 (= gamma)
+        c = 0.5 / (float(k[0, 0, key].float().square().sum()) * scale)
+        q[:, :, rows] = k[:, :, key:key + 1] * c
+        dO[:, :, rows] *= 8
+    Of, Mo, Zo, No, rdq, rdk, rdv, rdt, dabs = flash_oracle(q, k, v, 0.0, dO, scale, 0.5, True)
+    em = flash_reference_rounding(q, k, v, 0.0, dO, scale, 0.5, True)
+    assert (No[:, :, rows_a] == 3).all() and (No[:, :, rows_b] == 2).all()
+    o, dq, dk, dv, dtau = _run(q, k, v, 0.0, dO, scale, 0.5, True)
+    for name, got, want in (("O", o, Of), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert_bf16_close(to_np64(got), want, name, em.get(name))
+    # the tied keys' gradients, where a dropped tie term shows first
+    tied = [40, 100, 150, 60, 130]
+    assert_bf16_close(to_np64(dk)[:, :, tied], rdk[:, :, tied], "dk[tied]",
+                      None if em.get("dk") is None else em["dk"][:, :, tied])
+    assert_sum_close(float(dtau), rdt, dabs, BF16_ATOL, "dtau")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_flash_rows_with_every_key_tied(dev, dtype):
     """q = 0 and tau < 0 make every causal key of a row tie at the peak u = -tau (Nmax = i + 1)."""
