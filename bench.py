@@ -12,7 +12,8 @@ Also measured in the same run and reported on the same JSON line:
 * ``roofline``: the dominant kernel's algorithmic FLOP per launch over its
   average duration from HIP events on the launch stream;
 * ``silent_50``: the same step with 50 % of the 8256 causal 64x64 tiles planted
-  silent (zero key blocks {even j} \\ {96}, tau = 0.25) and the speedup;
+  silent (zero key blocks {even j} \\ {96}, tau = 0.25), the speedup, and its per-stage
+  kernel times;
 * ``fir``: standalone causal FIR (config C2, K [8,8,2048,64] bf16, per-head
   taps) in GB/s, rotating 20 input/output buffer pairs (640 MiB) so the 256 MB
   Infinity Cache cannot serve repeats, beside a device copy of the same bytes and the
@@ -722,6 +723,9 @@ def main():
     frac = plant_silent(ks, N)
     tile_stats = silent_tile_stats(q, ks, v, 0.25)
     step_s = flash_step_fn(q, ks, v, dO, 0.25)
+    # Per-stage times of the silent step first (one pass: the GPU is warm from the dense
+    # step, but the set-up above leaves it idle between launches), then the steps.
+    kern_s = kernel_times(q, ks, v, dO, 0.25, max(5, args.steps // 2))
     wall_s, ev_s, per_s = time_steps_detail(step_s, args.steps, args.warmup)
     del step_s, ks
 
@@ -781,7 +785,8 @@ def main():
         "kernels": kern,
         "silent_50": {"silent_fraction": round(frac, 4), "tau": 0.25, **tile_stats,
                       "ms_per_step": round(wall_s, 4), "event_ms_per_step": round(ev_s, 4),
-                      "step_event_ms": spread(per_s), "speedup": round(wall_ms / wall_s, 3)},
+                      "step_event_ms": spread(per_s), "speedup": round(wall_ms / wall_s, 3),
+                      "kernel_ms": {n: r["ms"] for n, r in kern_s.items()}},
         "fir": fir,
         "wide_head": {"config": C5, "ms_per_step": round(wall5, 4),
                       "step_event_ms": spread(per5),
