@@ -766,6 +766,13 @@ __device__ __forceinline__ float* rc_plane(const BwdParams& p, int64_t bh, int k
   return p.rc + (bh * 8 + k) * (int64_t)p.N;
 }
 
+// The forward's Z sums the bf16-rounded P that weighted V, and a row's weights are usually
+// dominated by its peak term.  The D <= 64 dK/dV kernel weights V by bf16(u^10) in the
+// peak-normalised units, the very rounded values Z sums, so Z normalises them consistently.
+// The D = 128 kernel rounds the whole weight x u^10 once, as the reference does with its
+// unrounded sum; there Z's rounding of the peak term (up to 2^-9) would offset every weight
+// of the row alike, so x = g/Z' with Z' = Z + (M^10 - bf16(M^10)), the peak term unrounded
+// (the same fp32 multiplies as the forward's u^10).
 template <int D, bool HAS_GAMMA>
 __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   constexpr int LPR = D / 8;  // lanes per row
@@ -800,7 +807,9 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
 #pragma unroll
   for (int o = 1; o < LPR; o <<= 1) dot += __shfl_xor(dot, o, 64);
   if (row < total && part == 0) {
-    const float M = p.M[row], Z = p.Z[row];
+    const float M = p.M[row];
+    const float Mp = D > 64 ? pow10f_(M) : 0.f;
+    const float Z = p.Z[row] + (__builtin_isfinite(Mp) ? Mp - (float)(bf16)Mp : 0.f);
     const float g = M > 0.f ? (HAS_GAMMA ? M / (M + p.gamma) : 1.f) : 0.f;
     const float x = g / Z;  // 0 on silent rows
     const float Dv = g > 0.f ? dot / g : 0.f;
