@@ -671,3 +671,12 @@ def test_flash_random_shapes_match_oracle(dev, case):
             assert_close(to_np64(got), want, F32_TOL, F32_TOL, name)
     tol = BF16_ATOL if dtype == torch.bfloat16 else F32_TOL
     assert_sum_close(float(dtau), rdt, dabs, tol, "dtau")
+
+
+# Draws of a wider seeded sweep whose d = 128 dV went past the bar (1.20 and 1.08) while the
+# backward normalised that form's weights by the forward's Z, whose peak term is bf16-rounded.
+@pytest.mark.parametrize("case", [
+    (1, 1, 462, 128, 0.0, 0.5, True, 128 ** -0.5, 2.0, False, torch.bfloat16),
+    (1, 2, 428, 128, 0.0, None, False, 128 ** -0.5, 1.0, False, torch.bfloat16)])
+def test_flash_d128_peaked_rows_match_oracle(dev, case):
+    test_flash_random_shapes_match_oracle(dev, case)
