@@ -33,8 +33,7 @@ brings the GPU to its steady clock, as the default run does --, fir, fir_sweep (
 copy from 32 to 512 MiB per launch), fir_fused (FIR + forward against the fused forward), copy (512 MiB device copy, the
 counter calibration), rows (row-fused score kernels on the C3 scores), lm (C3 LM step),
 mha6 (the 6-layer stack), ref (the reference's published shapes), kernels (per-stage HIP
-events at C4, C4 50 % silent and C5), pipe_probe (how far this GPU overlaps MFMA and VALU
-issue, pnfx_probe_pipe_overlap).
+events at C4, C4 50 % silent and C5).
 """
 from __future__ import annotations
 
@@ -351,32 +350,6 @@ def bench_copy(dev, mib=512, reps=20):
     return {"copy_bytes_each_way": mib << 20, "reps": reps}
 
 
-def bench_pipe_probe(dev, iters=4000):
-    """MFMA / VALU overlap of this GPU (pnfx_probe_pipe_overlap): for each mix, the loop's ms
-    with MFMAs only, FMAs only and both, and overlap = (t_m + t_v - t_both) / min(t_m, t_v)."""
-    import ctypes
-
-    from paper_01_anti_decoy_pnfirtau_amd import _lib
-
-    L = _lib.lib()
-    out = torch.empty(256 * 512, device=dev)
-    st = torch.cuda.current_stream().cuda_stream
-    rows = []
-    for waves in (1, 2):
-        for big in (0, 1):
-            for nm, nv in ((8, 32), (8, 64), (16, 64)):
-                ms = (ctypes.c_float * 3)()
-                _lib.check(L.pnfx_probe_pipe_overlap(waves, big, nm, nv, iters, out.data_ptr(),
-                                                     ms, st), "pnfx_probe_pipe_overlap")
-                tm, tv, tb = ms[0], ms[1], ms[2]
-                rows.append({"waves_per_simd": waves, "mfma": "32x32x16" if big else "16x16x32",
-                             "mfma_16x16x32_equiv_per_iter": nm, "fma_per_iter": nv,
-                             "ms_mfma": round(tm, 4), "ms_valu": round(tv, 4),
-                             "ms_both": round(tb, 4), "ms_sum": round(tm + tv, 4),
-                             "overlap": round((tm + tv - tb) / min(tm, tv), 3)})
-    return {"iters": iters, "workgroups": 256, "rows": rows}
-
-
 def profiled_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.
 
@@ -631,7 +604,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", choices=["flash", "flash_c5", "flash_silent", "fir", "fir_sweep", "fir_fused", "copy",
-                                       "lm", "mha6", "ref", "kernels", "rows", "pipe_probe"],
+                                       "lm", "mha6", "ref", "kernels", "rows"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -645,9 +618,6 @@ def main():
 
     if args.only == "copy":
         print(json.dumps(bench_copy(dev)))
-        return
-    if args.only == "pipe_probe":
-        print(json.dumps(bench_pipe_probe(dev)))
         return
     if args.only == "fir_sweep":
         print(json.dumps({"fir_size_sweep": bench_fir_sweep(dev)}), flush=True)

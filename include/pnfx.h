@@ -3,8 +3,7 @@
  *
  * Every entry point takes device pointers, element strides and sizes, and a
  * hipStream_t passed as `void*` (NULL = the legacy default stream).  Kernels are
- * enqueued on that stream; nothing blocks the host (the diagnostic
- * pnfx_probe_pipe_overlap aside) and nothing is allocated:
+ * enqueued on that stream; nothing blocks the host and nothing is allocated:
  * callers own every buffer, including the workspace of pnfx_flash_bwd (the one
  * exception, pnfx_flash_bwd_noalloc, uses a scratch array the library holds).
  *
@@ -210,12 +209,16 @@ int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int64_t qsh, i
  * hipMalloc).  No counterpart in the reference.  Same arguments and results as
  * pnfx_flash_bwd (bitwise the same outputs); the workspace is a scratch array of
  * PNFX_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on until the
- * process ends.  Shapes whose pnfx_flash_bwd_workspace_size exceeds that return PNFX_EINVAL
- * (C4, B=4 H=16 N=8192 D=64, needs 220 MB and fits).  Allocates nothing: the first call on
+ * process ends (it is part of the library's code object: every process that loads
+ * libpnfx.so holds it on each GPU the library initialises, whether or not this entry point
+ * is called).  Shapes whose pnfx_flash_bwd_workspace_size exceeds that return PNFX_EINVAL
+ * (C4, B=4 H=16 N=8192 D=64, needs 86 MB and fits).  Allocates nothing: the first call on
  * a device looks up the array's address there (the current device must be the stream's).
- * Calls that overlap on one GPU (different streams, or threads) share the array and race.
+ * Every call on one GPU uses the same array: calls that overlap on one GPU (different
+ * streams or threads, or a captured HIP graph replayed while another call or replay of one
+ * runs) race on it and give wrong results; serialise them.
  */
-#define PNFX_NOALLOC_SCRATCH_BYTES (256ll << 20)
+#define PNFX_NOALLOC_SCRATCH_BYTES (128ll << 20)
 int pnfx_flash_bwd_noalloc(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const void* k,
                            int64_t ksb, int64_t ksh, int64_t ksn, const void* v, int64_t vsb,
                            int64_t vsh, int64_t vsn, const void* o, int64_t osb, int64_t osh,
@@ -227,18 +230,6 @@ int pnfx_flash_bwd_noalloc(const void* q, int64_t qsb, int64_t qsh, int64_t qsn,
                            int64_t B, int64_t H, int64_t N, int64_t D, const float* tau,
                            float scale, float gamma, int has_gamma, int causal, int dtype,
                            void* stream);
-
-/*
- * Diagnostic, not on the attention path; no counterpart in the reference.  Times a
- * register-only loop of mfma_per_iter independent bf16 MFMAs (16x16x32, or half as many
- * 32x32x16 when mfma_32x32) and valu_per_iter independent fp32 FMAs, iters times, on one
- * workgroup per CU at waves_per_simd (1 or 2) waves per SIMD: ms[0] with the MFMAs only,
- * ms[1] with the FMAs only, ms[2] with both.  (mfma_per_iter, valu_per_iter) is one of
- * (8, 32), (8, 64), (16, 64).  out: device scratch of 256 * 512 floats.  Blocks until the
- * launches on stream finish.
- */
-int pnfx_probe_pipe_overlap(int waves_per_simd, int mfma_32x32, int mfma_per_iter,
-                            int valu_per_iter, int iters, float* out, float* ms, void* stream);
 
 #ifdef __cplusplus
 }

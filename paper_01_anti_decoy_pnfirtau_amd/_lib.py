@@ -15,7 +15,7 @@ ABI_VERSION = 3
 PNFX_F32 = 0
 PNFX_BF16 = 1
 PNFX_BWD_PREPARE, PNFX_BWD_DKDV, PNFX_BWD_DQ, PNFX_BWD_ALL = 1, 2, 4, 7
-PNFX_NOALLOC_SCRATCH_BYTES = 256 << 20
+PNFX_NOALLOC_SCRATCH_BYTES = 128 << 20
 
 _lib = None
 
@@ -45,7 +45,6 @@ def _declare(lib: ctypes.CDLL) -> None:
             + [vp, vp, vp, vp, i64, i64, i64, i64, vp, f32, f32, i32, i32, vp, i64, i32, i32, vp],
             i32),
         "pnfx_flash_fwd_workspace_size": ([i64, i64, i64, i64], i64),
-        "pnfx_probe_pipe_overlap": ([i32, i32, i32, i32, i32, vp, vp, vp], i32),
         "pnfx_flash_bwd_workspace_size": ([i64, i64, i64, i64], i64),
         "pnfx_flash_bwd": (
             [vp, i64, i64, i64] * 4
@@ -93,5 +92,5 @@ def exported_symbols() -> list[str]:
         "pnfx_pn_rows_fwd", "pnfx_pn_rows_bwd", "pnfx_flash_fwd", "pnfx_flash_fwd_fir",
         "pnfx_flash_fwd_workspace_size",
         "pnfx_flash_bwd_workspace_size", "pnfx_flash_bwd", "pnfx_flash_bwd_stages",
-        "pnfx_flash_bwd_noalloc", "pnfx_probe_pipe_overlap",
+        "pnfx_flash_bwd_noalloc",
     ]

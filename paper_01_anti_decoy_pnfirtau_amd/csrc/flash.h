@@ -35,10 +35,9 @@ struct BwdParams {
   const uint8_t* mask;
   float* rc;         // row constants [B*H*N][8], layout private to each dtype's kernels
   double* partials;  // tau partials, one per wave of the dq kernel (bf16: [B*H][N/BM][4])
-  void *qx, *dox;    // bf16, D <= 64: Q and dO rows scaled for the dK/dV products (by
-                     // x 2^9e and x 2^10e, x = g/Z, 2^e the row peak's power of two),
-                     // contiguous [B*H, N, D]
-  void* qs;          // bf16, D <= 64: Q rows scaled by 2^-e (exactly), for the scores there
+  void* qs;          // bf16, D <= 64: Q rows scaled by 2^-e (exactly; 2^e the power of two of
+                     // the row's peak), contiguous [B*H, N, D]: the dK/dV kernel's scores and
+                     // its dK product
   uint8_t* ktact;    // [B*H][nk64]: 64-key tiles with any active tile-mask entry (mask given)
   uint8_t* amap;     // [B*H][nq32][nk64] (mask given, N <= kAmapMaxN): bit 0 the sub-tile's
                      // activity, bit 1 + h a peak tie in its 32-key half h (dQ -> dK/dV)
@@ -60,8 +59,9 @@ inline int bwd_nkvb(int64_t N, int64_t D) {
 }
 // Workspace of the backward: row constants, tau partials (fp64, one per wave of the bf16 dq
 // kernel, four per workgroup; the fp32 kernels use one per 64 rows), and for D <= 64 the
-// three row-scaled copies of Q and dO that the bf16 dK/dV kernel reads, one activity byte
-// per 64-key tile, and the activity/tie map of the 32-query x 64-key sub-tiles.
+// peak-normalised copy of Q that the bf16 dK/dV kernel reads, one activity byte per 64-key
+// tile, and the activity/tie map of the 32-query x 64-key sub-tiles (written by a dQ wave of
+// 32 rows, so only where the dQ kernel runs two 16-row blocks per wave: D <= 64).
 // The activity/tie map of the backward (BwdParams::amap) is kept up to this sequence length:
 // N^2/2048 bytes per (b, h), 2 MiB at N = 65536.
 constexpr int64_t kAmapMaxN = 65536;
@@ -72,11 +72,13 @@ struct BwdWorkspace {
     const int64_t slots = B * H * ((N + rw - 1) / rw) * 4;
     rc_bytes = round256(B * H * N * 8 * 4);
     parts_bytes = round256(slots * 8);
-    xt_bytes = D <= 64 ? round256(B * H * N * D * 2) : 0;  // each of Qx, dOx, Qs
+    xt_bytes = D <= 64 ? round256(B * H * N * D * 2) : 0;  // Q 2^-e
     kt_bytes = round256(B * H * ((N + 63) / 64));
-    amap_bytes = N <= kAmapMaxN ? round256(B * H * ((N + 31) / 32) * ((N + 63) / 64)) : 0;
+    amap_bytes = (N <= kAmapMaxN && dq_qblocks(D) == 2)
+                     ? round256(B * H * ((N + 31) / 32) * ((N + 63) / 64))
+                     : 0;
   }
-  int64_t total() const { return rc_bytes + parts_bytes + 3 * xt_bytes + kt_bytes + amap_bytes; }
+  int64_t total() const { return rc_bytes + parts_bytes + xt_bytes + kt_bytes + amap_bytes; }
   static int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
 };
 

@@ -2,8 +2,11 @@
 //
 // Math (src/triton_pnfirtau.py:313-621): per query row i and key j <= i,
 //   s = fma(q_i . k_j, scale, -tau), u = relu(s), P = u^10 (four multiplies, no exp),
-//   mass += bf16(P), peak = max u, Nmax = #(u == peak);
+//   mass += bf16(P), Z = sum P + 1e-12 (unrounded), peak = max u, Nmax = #(u == peak);
 //   O_i = (sum_j bf16(P_ij) v_j) * gate_i / (mass_i + 1e-12), gate = peak/(peak + gamma).
+// O is normalised by the mass of the rounded weights that multiply V (a true convex
+// combination, so the flash identity of the backward holds for the weights actually used);
+// the stored Z is the reference's unrounded sum, which the backward's gate/Z uses.
 // There is no running rescale (unlike softmax), so mass and peak stay lane-local for the
 // whole key loop and are reduced across lanes once, in the epilogue.
 //
@@ -188,13 +191,11 @@ struct KVBuf {
   bf16* kr = nullptr;
 };
 
-// One LDS buffer of the dK/dV kernel: a query tile of Q and dO, for D <= 64 also of their
-// row-scaled copies, and its row-constant planes.
+// One LDS buffer of the dK/dV kernel: a query tile of Q (for D <= 64 scaled by 2^-e per row)
+// and dO, and its row-constant planes.
 struct QBuf {
   bf16* q;
   bf16* o;
-  bf16* qx;
-  bf16* ox;
   float* rc;  // [planes][64 rows]
 };
 
@@ -353,13 +354,9 @@ __global__ __launch_bounds__(256) void flash_key_norm_kernel(FwdParams p) {
   if (lane == 0) p.knorm[tile] = sqrtf(ss);
 }
 
-// Without tie counting the forward needs no rectified copy of the scores.  Each query row's
-// maximum of u = relu(s) is max(0, max s): an integer max from 0 over the raw bit patterns
-// (positive floats order as their bits; negative ones are negative integers).  P = u^10 is
-// formed from the raw score: t = s |s| carries the sign of s into the chain t^2, t^4,
-// t^4 t = sign(s) s^10 -- for s > 0 the very multiplies of u^2, u^4, u^8, u^8 u^2 -- and a
-// signed 16-bit max with 0 on the packed bf16 values turns the negative ones (s < 0, and the
-// masked -1) into +0: half a VALU op per score instead of a rectifier on every score.
+// Each query row's maximum of u = relu(s) is max(0, max s): an integer max from 0 over the
+// raw bit patterns (positive floats order as their bits; negative ones are negative
+// integers), so the silent-half test needs no rectified copy of the scores.
 // Bit patterns through by-value helpers: clang's __builtin_bit_cast applied directly to an
 // ext_vector element (v[i]) reads element 0 whatever i is.
 __device__ __forceinline__ int f2i(float x) { return __builtin_bit_cast(int, x); }
@@ -375,26 +372,6 @@ __device__ __forceinline__ void row_max_kq(const f32x4 (&s)[2][2], float (&tm)[2
       for (int i = 0; i < 4; ++i) mx = max(mx, f2i(s[kk][qb][i]));
     tm[qb] = i2f(mx);
   }
-}
-__device__ __forceinline__ float pow10_signed(float s) {
-  const float t = s * __builtin_fabsf(s);
-  const float t2 = t * t;
-  const float t4 = t2 * t2;
-  return t4 * t;
-}
-// Two floats to a packed bf16 pair (RNE), negative results to +0.
-__device__ __forceinline__ uint32_t pack2_relu(float a, float b) {
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  typedef short s16x2 __attribute__((ext_vector_type(2)));
-  const bf16x2 v = __builtin_convertvector((f32x2){a, b}, bf16x2);
-  const s16x2 z = {0, 0};
-  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(s16x2, v), z));
-}
-__device__ __forceinline__ bf16x8 pack8_relu(float a0, float a1, float a2, float a3, float b0,
-                                             float b1, float b2, float b3) {
-  const u32x4 w = {pack2_relu(a0, a1), pack2_relu(a2, a3), pack2_relu(b0, b1), pack2_relu(b2, b3)};
-  return __builtin_bit_cast(bf16x8, w);
 }
 // max of two non-negative floats as an integer max (no canonicalising operand copies)
 __device__ __forceinline__ float max_nonneg(float a, float b) {
@@ -486,6 +463,10 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
   }
   float mrun[2] = {0.f, 0.f};
   int cnt[2] = {0, 0};
+  // The unrounded mass sum P in fp32, the reference's normaliser (src/triton_pnfirtau.py:405):
+  // the stored Z, from which the backward forms x = gate/Z.  O itself is normalised by the
+  // MFMA mass of the rounded P above.
+  float zf[2] = {0.f, 0.f};
 
   const int kv_end = CAUSAL ? min(m0 + BM, N) : N;
   const int ntiles = (kv_end + BN - 1) / BN;
@@ -664,15 +645,18 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
             cnt[qb] = c;
           }
           mrun[qb] = mnew;
-          if constexpr (COUNT)
-            pf[qb] = pack8(pow10f_(s[0][qb][0]), pow10f_(s[0][qb][1]), pow10f_(s[0][qb][2]),
-                           pow10f_(s[0][qb][3]), pow10f_(s[1][qb][0]), pow10f_(s[1][qb][1]),
-                           pow10f_(s[1][qb][2]), pow10f_(s[1][qb][3]));
-          else
-            pf[qb] = pack8_relu(
-                pow10_signed(s[0][qb][0]), pow10_signed(s[0][qb][1]), pow10_signed(s[0][qb][2]),
-                pow10_signed(s[0][qb][3]), pow10_signed(s[1][qb][0]), pow10_signed(s[1][qb][1]),
-                pow10_signed(s[1][qb][2]), pow10_signed(s[1][qb][3]));
+          // P = u^10 (u = relu(s); COUNT has rectified s already), summed unrounded into zf
+          float pw[2][4];
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float u = COUNT ? s[kk][qb][i] : relu_mfma(s[kk][qb][i]);
+              pw[kk][i] = pow10f_(u);
+              zf[qb] += pw[kk][i];
+            }
+          pf[qb] = pack8(pw[0][0], pw[0][1], pw[0][2], pw[0][3], pw[1][0], pw[1][1], pw[1][2],
+                         pw[1][3]);
         }
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
@@ -709,9 +693,11 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
     }
     // row 0 of the mass block lives in lane r16 (lane group 0), register 0
     const float ms = __shfl(accm[qb][0], r16, 64);
+    float zr = zf[qb] + __shfl_xor(zf[qb], 16, 64);
+    zr += __shfl_xor(zr, 32, 64);
     const float gate = Mx > 0.f ? (p.has_gamma ? Mx / (Mx + p.gamma) : 1.f) : 0.f;
-    const float z = ms + 1e-12f;
-    const float so = gate / z;
+    const float so = gate / (ms + 1e-12f);
+    const float z = zr + 1e-12f;
     const int qrow = qrow0 + 16 * qb + r16;
     if (qrow < N) {
 #pragma unroll
@@ -739,22 +725,22 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
 
 // ------------------------------------------------------------------------------ backward
 // Row constants.  With D_i = <dO_i, O_i>/g_i (the flash identity of
-// src/triton_pnfirtau.py:575-577) and x_i = g_i/Z_i, the score gradient (:580-586) is
-//   dS_ij = 10 scale x_i [u_ij^9 (dW_ij - D_i) + [u_ij == M_i] G''_i/Nmax_i],
-//   G''_i = D_i gate'(M_i) / (10 x_i),
-// which is how the dQ kernel forms it: the dW MFMA accumulator starts at -D_i, the bracket
-// costs one FMA per score after the power chain, and the row factor is applied once, at
-// the end: 10 scale x_i to dQ, 10 x_i to the tau partials (sums of du = dS/scale, so that
-// dtau = -sum du needs no division by scale).  The dK/dV kernel needs the row factor
-// inside its sums over rows; there, with rho_i = x_i^(1/10), a = rho u and
-// kappa_i = 10 scale rho_i, the dV weight is w = u^10 x = a^10 and
-//   dS_ij = a^9 (kappa_i dW_ij - kappa_i D_i) + [u_ij == M_i] G_i/Nmax_i,
-//   G_i = D_i gate'(M_i) scale.
-// The bf16 row constants are eight planes of N floats per (b, h): M, -D, G'', x, rho, kappa,
-// -kappa D, and G/Nmax (written by the dQ kernel, which counts the ties).  For D <= 64 the
-// dK/dV kernel forms its scores scaled by 2^-e per row (see pow9_unit), and planes 4, 5 hold
-// M 2^-e and -tau 2^-e instead of rho and kappa, plane 6 is not written (nor rho, a powf,
-// computed), and plane 7 holds G'' 2^-9e / Nmax.
+// src/triton_pnfirtau.py:575-577), x_i = g_i/Z_i and the score gradient of :580-586,
+//   du_ij = 10 x_i u_ij^9 (dW_ij - D_i) + [u_ij == M_i] D_i gate'(M_i)/Nmax_i,
+//   dS_ij = scale du_ij,  w_ij = x_i u_ij^10.
+// The gradient kernels round w and dS to bf16 once, before their products, as the reference
+// does (:566-571, :598-600), and form them from the scores peak-normalised per row: with
+// M = m 2^e (m in [0.5, 1)) the scores are computed scaled by 2^-e (exactly: a power of two
+// folded into the operands), so every scaled score is below 1 (see pow9_unit) and u9s =
+// u^9 2^-9e.  The dQ kernel rounds f du = (10 f x 2^9e) u9s (dW - D) + tie f D gate'/Nmax (f =
+// scale, or 1 when scale = 0 so that the tau partials keep du).  The D <= 64 dK/dV kernel
+// rounds w = (x 2^10e u9s) s_scaled and dS 2^e (its dK product takes Q 2^-e); the D = 128 one
+// uses a = rho u (rho = x^(1/10), kappa = 10 scale rho): w = a^10, dS = a^9 (kappa dW -
+// kappa D) + tie.
+// The row constants are eight planes of N floats per (b, h): M, -D, D gate'(M) (the tie
+// gradient of du for a single tie), x, then for D <= 64: M 2^-e, -tau 2^-e, x 2^10e; for
+// D = 128: rho, kappa, -kappa D; plane 7 is the dK/dV kernel's tie term of dS per tied key
+// (for D <= 64 times 2^e), written by the dQ kernel, which counts the ties.
 // Exponent e of a row peak, M = m 2^e with m in [0.5, 1) (0 for silent rows), kept within
 // +-64: a peak below 2^-64 then scales to below 1 all the same, and one above 2^64 has already
 // overflowed the forward's u^10.
@@ -766,13 +752,6 @@ __device__ __forceinline__ float* rc_plane(const BwdParams& p, int64_t bh, int k
   return p.rc + (bh * 8 + k) * (int64_t)p.N;
 }
 
-// The forward's Z sums the bf16-rounded P that weighted V, and a row's weights are usually
-// dominated by its peak term.  The D <= 64 dK/dV kernel weights V by bf16(u^10) in the
-// peak-normalised units, the very rounded values Z sums, so Z normalises them consistently.
-// The D = 128 kernel rounds the whole weight x u^10 once, as the reference does with its
-// unrounded sum; there Z's rounding of the peak term (up to 2^-9) would offset every weight
-// of the row alike, so x = g/Z' with Z' = Z + (M^10 - bf16(M^10)), the peak term unrounded
-// (the same fp32 multiplies as the forward's u^10).
 template <int D, bool HAS_GAMMA>
 __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   constexpr int LPR = D / 8;  // lanes per row
@@ -808,22 +787,21 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
   for (int o = 1; o < LPR; o <<= 1) dot += __shfl_xor(dot, o, 64);
   if (row < total && part == 0) {
     const float M = p.M[row];
-    const float Mp = D > 64 ? pow10f_(M) : 0.f;
-    const float Z = p.Z[row] + (__builtin_isfinite(Mp) ? Mp - (float)(bf16)Mp : 0.f);
     const float g = M > 0.f ? (HAS_GAMMA ? M / (M + p.gamma) : 1.f) : 0.f;
-    const float x = g / Z;  // 0 on silent rows
+    const float x = g / p.Z[row];  // 0 on silent rows
     const float Dv = g > 0.f ? dot / g : 0.f;
     float dgate = 0.f;
     if (HAS_GAMMA && M > 0.f) dgate = p.gamma / ((M + p.gamma) * (M + p.gamma));
     const int64_t bh = row / p.N, i = row % p.N;
     rc_plane(p, bh, 0)[i] = M;
     rc_plane(p, bh, 1)[i] = -Dv;
-    rc_plane(p, bh, 2)[i] = x > 0.f ? Dv * dgate / (10.f * x) : 0.f;
+    rc_plane(p, bh, 2)[i] = Dv * dgate;
     rc_plane(p, bh, 3)[i] = x;
-    if (D <= 64) {  // the peak-normalised scores of the dK/dV kernel (plane 6 unused)
+    if (D <= 64) {  // the peak-normalised form of the dK/dV kernel
       const int e = peak_exponent(M);
       rc_plane(p, bh, 4)[i] = __builtin_amdgcn_ldexpf(M, -e);
       rc_plane(p, bh, 5)[i] = __builtin_amdgcn_ldexpf(-p.tau[0], -e);
+      rc_plane(p, bh, 6)[i] = __builtin_amdgcn_ldexpf(x, 10 * e);
     } else {  // the a = rho u form of the D = 128 dK/dV kernel
       const float rho = powf(x, 0.1f);
       const float kappa = 10.f * p.scale * rho;
@@ -846,32 +824,34 @@ __device__ __forceinline__ float pow9_unit(float s) {
   return (t2 * t2) * s;
 }
 
-// dS/(10 scale x 2^9e) for the 8 scores a lane holds in query block qb of one 32-key half
-// tile of the dQ kernel (S^T layout, one query row per lane, scores scaled by 2^-e), written
-// over dw = dW - D: u^9 dw + [u == M] G'' (u, M, G'' in the scaled units).  Also counts the
-// row's peak ties.
+// f du (see the row constants) for the 8 scores a lane holds in query block qb of one 32-key
+// half tile of the dQ kernel (S^T layout, one query row per lane, scores scaled by 2^-e),
+// written over dw = dW - D: (u9s R) dw + [u == M] T with R = 10 f x 2^9e and T the tie term
+// (u, M in the scaled units).  Also counts the row's peak ties.
 template <int QB>
 __device__ __forceinline__ void ds_kq(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB], int (&cnt)[QB],
-                                      const float (&rM)[QB], const float (&rG)[QB], int qb) {
+                                      const float (&rM)[QB], const float (&rR)[QB],
+                                      const float (&rT)[QB], int qb) {
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float u9 = pow9_unit(s[kk][qb][i]);
-      const bool tie = s[kk][qb][i] == rM[qb];  // M > 0; G'' = 0 on silent rows
-      dw[kk][qb][i] = __builtin_fmaf(u9, dw[kk][qb][i], tie ? rG[qb] : 0.f);
+      const float a = pow9_unit(s[kk][qb][i]) * rR[qb];
+      const bool tie = s[kk][qb][i] == rM[qb];  // M > 0; T = 0 on silent rows
+      dw[kk][qb][i] = __builtin_fmaf(a, dw[kk][qb][i], tie ? rT[qb] : 0.f);
       cnt[qb] += tie ? 1 : 0;
     }
 }
 
 // ds_kq without the peak-tie term, for a query block where no row of the wave has a key of
-// the half tile at its peak: dS/(10 scale x 2^9e) = u^9 (dW - D).
+// the half tile at its peak: f du = (u9s R) (dW - D).
 template <int QB>
-__device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB], int qb) {
+__device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][QB], f32x4 (&dw)[2][QB],
+                                            const float (&rR)[QB], int qb) {
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dw[kk][qb][i] = pow9_unit(s[kk][qb][i]) * dw[kk][qb][i];
+    for (int i = 0; i < 4; ++i) dw[kk][qb][i] = (pow9_unit(s[kk][qb][i]) * rR[qb]) * dw[kk][qb][i];
 }
 
 // Whether some lane of the wave holds, in query block qb, a score tied at its row's peak M on
@@ -883,30 +863,31 @@ __device__ __forceinline__ void ds_kq_notie(const f32x4 (&s)[2][QB], f32x4 (&dw)
 // many blocks as it would per 32-row half tile.
 template <int QB>
 __device__ __forceinline__ bool peak_tie(const f32x4 (&s)[2][QB], const float (&rM)[QB],
-                                         const float (&rG)[QB], int qb) {
+                                         const float (&rT)[QB], int qb) {
   int mx = f2i(s[0][qb][0]);
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
     for (int i = 0; i < 4; ++i) mx = max(mx, f2i(s[kk][qb][i]));
-  return __any(mx >= f2i(rM[qb]) && rG[qb] != 0.f);
+  return __any(mx >= f2i(rM[qb]) && rT[qb] != 0.f);
 }
 
 // dQ: query-parallel, same tiling as the forward (4 waves x 32 rows, 64-key tiles), K and V
 // tiles software-pipelined through LDS (double-buffered when it fits).
 //
-// Peak ties.  A key tied at the row's peak gets the extra gradient G/Nmax.  The forward
-// does not count ties, so the first pass over the keys uses the whole-row G per tied key
-// while it counts the ties (one compare serves both).  Afterwards G/Nmax replaces G in the
-// row constants (for the dK/dV kernel) and the tau partial is corrected to G per row.  A row
-// with two or more ties got too much tie gradient in dQ: if the workgroup has any such row
-// (rare: duplicated keys), it runs the key loop a second time with G/Nmax.
+// Peak ties.  A key tied at the row's peak gets the extra gradient D gate'/Nmax.  The forward
+// does not count ties, so the first pass over the keys gives every tied key the whole-row
+// term while it counts the ties (one compare serves both).  Afterwards the per-key share
+// goes to the row constants (for the dK/dV kernel) and the tau partial is corrected to one
+// whole-row term per row.  A row with two or more ties got too much tie gradient in dQ: if
+// the workgroup has any such row (rare: duplicated keys), it runs the key loop a second time
+// with the per-key share.
 // At D = 128 the dQ accumulators and the Q/dO fragments of 32 rows need more than the 256
 // registers a wave has at two workgroups per CU, so each wave takes 16 rows there (64-row
 // workgroups, two per CU) instead of running one 128-row workgroup per CU.
 template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
-  constexpr bool XT = D <= 64;  // writes the row-scaled Q and dO of the dK/dV kernel
+  constexpr bool XT = D <= 64;  // writes the peak-normalised Q of the dK/dV kernel
   // Query rows per wave: 32 (two 16-row MFMA blocks) up to D = 64; 16 at D = 128, where the
   // dQ accumulators and the Q/dO fragments of 32 rows would not fit two workgroups per CU.
   constexpr int QB = dq_qblocks(D), RPW = 16 * QB;
@@ -938,23 +919,22 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   const bool has_rows = qrow0 < N;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
-  const float ds_mult = 10.f * scale;  // the score loops form dS/(10 scale x)
+  // The loops form f du, rounded to bf16 once: with f = scale that is dS, rounded where the
+  // reference rounds it; at scale = 0 (dS = 0), f = 1 keeps du for the tau partials.
+  const float fdu = scale != 0.f ? scale : 1.f;
   const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
 
   bf16x8 qf[QB][KS], dof[QB][KS];
   // Row constants.  The scores of row i are formed scaled by 2^-e_i, e_i the exponent of its
-  // peak M_i (see pow9_unit): rM and rG (the tie term) are in those units, rE holds e_i, and
-  // the row factor 10 scale x_i 2^(9 e_i) is applied to dQ and the tau partial at the end.
-  // rG0 keeps G'' unscaled for the row-constant plane of the dK/dV kernel.
-  float rM[QB], rG[QB], rG0[QB], rX[QB];
+  // peak M_i (see pow9_unit): rM is the scaled peak, rR = 10 f x_i 2^(9 e_i) turns u9s into
+  // the factor of dW - D, rT is the tie term (f D gate'; divided by the tie count in a second
+  // pass), rT0 the whole-row term and rDg = D gate' for the dK/dV kernel's plane.
+  float rM[QB], rR[QB], rT[QB], rT0[QB], rDg[QB];
   int rE[QB];
   f32x4 dw_init[QB];  // -D: the dW accumulator starts there
   f32x4 s_init[QB];   // the score accumulator starts at -tau 2^-e (scale folded into Q)
   float sc_e[QB], nt_e[QB];  // scale 2^-e and -tau 2^-e, for scales that are not folded
-  // D <= 64, for the dK/dV kernel (which runs next): the rows of Q scaled by 2^-e (its
-  // scores), by x 2^9e (dK) and of dO by x 2^10e (dV), x = g/Z.
-  bf16* Qx = XT ? static_cast<bf16*>(p.qx) + (int64_t)bh * N * D : nullptr;
-  bf16* dOx = XT ? static_cast<bf16*>(p.dox) + (int64_t)bh * N * D : nullptr;
+  // D <= 64, for the dK/dV kernel (which runs next): the rows of Q scaled by 2^-e.
   bf16* Qs = XT ? static_cast<bf16*>(p.qs) + (int64_t)bh * N * D : nullptr;
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
@@ -962,11 +942,13 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
     const bool rok = row < N;
     const float M = rok ? rc_plane(p, bh, 0)[row] : 0.f;
     const float nxd = rok ? rc_plane(p, bh, 1)[row] : 0.f;
-    rG0[qb] = rok ? rc_plane(p, bh, 2)[row] : 0.f;
-    rX[qb] = rok ? rc_plane(p, bh, 3)[row] : 0.f;
+    rDg[qb] = rok ? rc_plane(p, bh, 2)[row] : 0.f;
+    const float x = rok ? rc_plane(p, bh, 3)[row] : 0.f;
     rE[qb] = peak_exponent(M);
     rM[qb] = __builtin_amdgcn_ldexpf(M, -rE[qb]);
-    rG[qb] = __builtin_amdgcn_ldexpf(rG0[qb], -9 * rE[qb]);
+    rR[qb] = __builtin_amdgcn_ldexpf(10.f * fdu * x, 9 * rE[qb]);
+    rT0[qb] = fdu * rDg[qb];
+    rT[qb] = rT0[qb];
     sc_e[qb] = __builtin_amdgcn_ldexpf(scale, -rE[qb]);
     nt_e[qb] = __builtin_amdgcn_ldexpf(ntau, -rE[qb]);
     s_init[qb] = PS ? f32x4{nt_e[qb], nt_e[qb], nt_e[qb], nt_e[qb]} : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -977,14 +959,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       const bool ok = rok && col < D;
       qf[qb][ks] = ok ? ld16(Q + (int64_t)row * p.qsn + col) : zero_bf16x8();
       dof[qb][ks] = ok ? ld16(dO + (int64_t)row * p.dosn + col) : zero_bf16x8();
-      if (XT && ok) {
-        const int64_t o = (int64_t)row * D + col;
-        *reinterpret_cast<bf16x8*>(Qx + o) =
-            scale_frag(qf[qb][ks], __builtin_amdgcn_ldexpf(rX[qb], 9 * rE[qb]));
-        *reinterpret_cast<bf16x8*>(dOx + o) =
-            scale_frag(dof[qb][ks], __builtin_amdgcn_ldexpf(rX[qb], 10 * rE[qb]));
-        *reinterpret_cast<bf16x8*>(Qs + o) = scale_frag(qf[qb][ks], __builtin_amdgcn_ldexpf(1.f, -rE[qb]));
-      }
+      if (XT && ok)
+        *reinterpret_cast<bf16x8*>(Qs + (int64_t)row * D + col) =
+            scale_frag(qf[qb][ks], __builtin_amdgcn_ldexpf(1.f, -rE[qb]));
       if (PS) qf[qb][ks] = scale_frag(qf[qb][ks], sc_e[qb]);  // a power of two: exact
     }
   }
@@ -1109,11 +1086,11 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
         if (masked) mask_kq(s, n0, hf, qrow0, N, CAUSAL, g, r16);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-          if (peak_tie(s, rM, rG, qb)) {
-            ds_kq(s, dw, cnt, rM, rG, qb);
+          if (peak_tie(s, rM, rT, qb)) {
+            ds_kq(s, dw, cnt, rM, rR, rT, qb);
             code |= 2 << hf;
           } else {
-            ds_kq_notie(s, dw, qb);
+            ds_kq_notie(s, dw, rR, qb);
           }
         }
         bf16x8 pf[QB];
@@ -1143,8 +1120,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   }
   if (pass == 1) break;
 
-  // Tie counts per row (the four lane groups of a row), G/Nmax for the dK/dV kernel, and
-  // the tau partial: the MFMA sum holds Nmax G'' per row for ties whose gradient is G''.
+  // Tie counts per row (the four lane groups of a row), the dK/dV kernel's tie term per tied
+  // key, and the tau partial: the MFMA sum holds f du over the row with Nmax whole-row tie
+  // terms where one belongs.
   double dsum = 0.0;
   bool multi = false;
 #pragma unroll
@@ -1154,18 +1132,18 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
     c += __shfl_xor(c, 32, 64);
     const int qrow = qrow0 + 16 * qb + r16;
     if (g == 0 && qrow < N) {
-      // G''/Nmax for the dK/dV kernel with the row-scaled tiles (D <= 64), else G/Nmax
-      // G'' 2^-9e / Nmax for the dK/dV kernel's peak-normalised form (D <= 64), else G/Nmax
-      rc_plane(p, bh, 7)[qrow] = c > 0 ? (XT ? rG[qb] : rG0[qb] * (ds_mult * rX[qb])) / (float)c : 0.f;
+      // dS per tied key (D <= 64: times 2^e, the dK/dV kernel's units)
+      const float ts = scale * rDg[qb];
+      rc_plane(p, bh, 7)[qrow] = c > 0 ? (XT ? __builtin_amdgcn_ldexpf(ts, rE[qb]) : ts) / (float)c : 0.f;
       double rs = (double)adt[qb][0];
-      if (c > 1) rs -= (double)rG[qb] * (double)(c - 1);
-      dsum += rs * (double)__builtin_amdgcn_ldexpf(rX[qb], 9 * rE[qb]);
+      if (c > 1) rs -= (double)rT0[qb] * (double)(c - 1);
+      dsum += rs;
     }
-    multi = multi || (c > 1 && rG[qb] != 0.f);
-    rG[qb] = c > 0 ? rG[qb] / (float)c : 0.f;  // for a second pass
+    multi = multi || (c > 1 && rT0[qb] != 0.f);
+    rT[qb] = c > 0 ? rT0[qb] / (float)c : 0.f;  // for a second pass
   }
-  // sum of du = dS / scale (no division by scale: scale may be 0)
-  dsum = wave_sum_d(dsum) * 10.0;
+  // sum of du (f du / f)
+  dsum = wave_sum_d(dsum) / (double)fdu;
   if (lane == 0) p.partials[((int64_t)bh * nqb + qblk) * 4 + w] = dsum;
   // Second pass only if some row of the workgroup has several ties (also a barrier: the
   // last tile's LDS buffer is free before the first tile is staged again).
@@ -1177,10 +1155,10 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   }
 
   bf16* dQ = static_cast<bf16*>(p.dq) + b * p.dqsb + h * p.dqsh;
+  const float rowf = scale != 0.f ? 1.f : 0.f;  // dS = scale du: the sums are dQ (or 0)
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int qrow = qrow0 + 16 * qb + r16;
-    const float rowf = ds_mult * __builtin_amdgcn_ldexpf(rX[qb], 9 * rE[qb]);
     if (qrow < N) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
@@ -1279,44 +1257,50 @@ __device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], c
   }
 }
 
-// D <= 64 form: the scores are peak-normalised (scaled by 2^-e per row, see pow9_unit) and
-// the Q and dO tiles of the dK and dV products are staged scaled by x 2^9e and x 2^10e.  The
-// dV weight u^10 over s and dS/(10 scale x 2^9e) = u^9 dw + [u == M] G''/Nmax over
-// dw = dW - D, in the scaled units.  rc holds the planes (M 2^-e, -D, G'' 2^-9e/Nmax).
+// D <= 64 form: the scores are peak-normalised (scaled by 2^-e per row, see pow9_unit).  With
+// aw = u9s x 2^10e = x u^9 2^e (rc plane 4 holds x 2^10e), the dV weight w = aw s = x u^10 is
+// written over s, and dS 2^e = (aw c) dw + [u == M] T 2^e over dw = dW - D, c = 10 scale:
+// both are the reference's values, to be rounded to bf16 once (dS 2^e rounds as dS does, and
+// the dK product takes Q 2^-e).  rc holds the planes (M 2^-e, -D, T 2^e per tied key,
+// -tau 2^-e, x 2^10e).
 template <int KB>
 __device__ __forceinline__ void w_ds_qk_x(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const float* rc,
-                                          int pitch, int r4) {
+                                          int pitch, int r4, float c) {
 #pragma unroll
   for (int qq = 0; qq < 2; ++qq) {
     const f32x4 m4 = *reinterpret_cast<const f32x4*>(rc + r4 + 4 * qq);
     const f32x4 t4 = *reinterpret_cast<const f32x4*>(rc + 2 * pitch + r4 + 4 * qq);
+    const f32x4 x4 = *reinterpret_cast<const f32x4*>(rc + 4 * pitch + r4 + 4 * qq);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const float sv = s[qq][kb][i];
-        const float u9 = pow9_unit(sv);
-        s[qq][kb][i] = u9 * sv;                           // 0 for sv <= 0 (u9 = 0)
-        const float tie = (sv == m4[i]) ? t4[i] : 0.f;  // M > 0; G'' = 0 on silent rows
-        dw[qq][kb][i] = __builtin_fmaf(u9, dw[qq][kb][i], tie);
+        const float aw = pow9_unit(sv) * x4[i];
+        s[qq][kb][i] = aw * sv;                           // 0 for sv <= 0 (u9s = 0)
+        const float tie = (sv == m4[i]) ? t4[i] : 0.f;  // M > 0; T = 0 on silent rows
+        dw[qq][kb][i] = __builtin_fmaf(aw * c, dw[qq][kb][i], tie);
       }
   }
 }
 
 // w_ds_qk_x without the peak-tie term (no row of the half has a key of this wave at its peak).
 template <int KB>
-__device__ __forceinline__ void w_ds_qk_x_notie(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB]) {
+__device__ __forceinline__ void w_ds_qk_x_notie(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB],
+                                                const float* rc, int pitch, int r4, float c) {
 #pragma unroll
-  for (int qq = 0; qq < 2; ++qq)
+  for (int qq = 0; qq < 2; ++qq) {
+    const f32x4 x4 = *reinterpret_cast<const f32x4*>(rc + 4 * pitch + r4 + 4 * qq);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const float sv = s[qq][kb][i];
-        const float u9 = pow9_unit(sv);
-        s[qq][kb][i] = u9 * sv;
-        dw[qq][kb][i] = u9 * dw[qq][kb][i];
+        const float aw = pow9_unit(sv) * x4[i];
+        s[qq][kb][i] = aw * sv;
+        dw[qq][kb][i] = (aw * c) * dw[qq][kb][i];
       }
+  }
 }
 
 // w_ds_qk without the peak-tie term.
@@ -1370,9 +1354,9 @@ __device__ __forceinline__ int ordered_ktile(const uint8_t* act, int nk64, int e
 
 template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
-  // D <= 64: the row factor x = g/Z rides on staged copies of Q and dO (written by the dQ
-  // kernel) for the dK and dV products, which saves two VALU ops per score; at D = 128 the
-  // extra tiles would not fit two workgroups per CU, and the rescaled form a = rho u is used.
+  // D <= 64: the scores are peak-normalised per row (from the dQ kernel's copy Q 2^-e, which
+  // also serves the dK product) and the weights formed from u9s; D = 128 uses a = rho u on the
+  // raw Q tile.  Either way the tiles are Q (scaled or not) and dO.
   constexpr bool XT = D <= 64;
   constexpr int KPW = DkdvCfg<D>::KPW, KB = DkdvCfg<D>::KB, BNK = DkdvCfg<D>::BNK;
   constexpr int BMQ = 64;
@@ -1381,24 +1365,19 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   constexpr int DB = D / 16;
   // Two LDS buffers, as separate objects: the compiler then knows that the direct-to-LDS
   // loads filling one buffer do not write the other, and does not make the reads of the
-  // current tile wait for the prefetch of the next one.  Row constants are five planes
-  // (M, rho, kappa, -kappa D, G/Nmax) of the tile's rows: a lane reads the four consecutive
-  // rows its registers cover as one f32x4 per plane (broadcast within a 16-lane group; the
-  // four groups' rows are 8 apart, in different banks).
-  // XT: four planes (M 2^-e, -D, G'' 2^-9e/Nmax, -tau 2^-e) of the peak-normalised form.
-  constexpr int NPL = XT ? 4 : 5;
-  constexpr int XS = XT ? BMQ * DK : 8;  // scaled tiles (unused at D = 128)
+  // current tile wait for the prefetch of the next one.  Row constants are five planes of the
+  // tile's rows: a lane reads the four consecutive rows its registers cover as one f32x4 per
+  // plane (broadcast within a 16-lane group; the four groups' rows are 8 apart, in different
+  // banks).  XT: (M 2^-e, -D, T 2^e per tied key, -tau 2^-e, x 2^10e); D = 128: (M, rho,
+  // kappa, -kappa D, G/Nmax).
+  constexpr int NPL = 5;
   __shared__ __attribute__((aligned(16))) bf16 Qs0[BMQ * DK];
   __shared__ __attribute__((aligned(16))) bf16 dOs0[BMQ * DK];
-  __shared__ __attribute__((aligned(16))) bf16 Qxs0[XS];
-  __shared__ __attribute__((aligned(16))) bf16 dOxs0[XS];
   __shared__ __attribute__((aligned(16))) float RC0[NPL * BMQ];
   __shared__ __attribute__((aligned(16))) bf16 Qs1[BMQ * DK];
   __shared__ __attribute__((aligned(16))) bf16 dOs1[BMQ * DK];
-  __shared__ __attribute__((aligned(16))) bf16 Qxs1[XS];
-  __shared__ __attribute__((aligned(16))) bf16 dOxs1[XS];
   __shared__ __attribute__((aligned(16))) float RC1[NPL * BMQ];
-  const QBuf buf0{Qs0, dOs0, Qxs0, dOxs0, RC0}, buf1{Qs1, dOs1, Qxs1, dOxs1, RC1};
+  const QBuf buf0{Qs0, dOs0, RC0}, buf1{Qs1, dOs1, RC1};
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, provably uniform
@@ -1410,16 +1389,12 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const bf16* K = static_cast<const bf16*>(p.k) + b * p.ksb + h * p.ksh;
   const bf16* V = static_cast<const bf16*>(p.v) + b * p.vsb + h * p.vsh;
   const bf16* dO = static_cast<const bf16*>(p.dout) + b * p.dosb + h * p.dosh;
-  // Staging of the row constants: wave w copies plane w of the tile's rows (XT: workspace
-  // planes 4, 1, 7, 5 = M 2^-e, -D, G'' 2^-9e/Nmax, -tau 2^-e; else 0, 4, 5, 6, 7 = M, rho,
-  // kappa, -kappa D, G/Nmax, wave 0 also the last).
+  // Staging of the row constants: wave w copies one plane of the tile's rows, wave 0 also the
+  // fifth (XT: workspace planes 4, 1, 7, 5, 6; D = 128: 0, 4, 5, 6, 7).
   const float* RCgw = rc_plane(p, bh, XT ? (w == 0 ? 4 : w == 2 ? 7 : w == 3 ? 5 : 1)
                                          : (w == 0 ? 0 : 3 + w));
-  const float* RCg4 = rc_plane(p, bh, 7);
-  // XT: the scaled copies written by the dQ kernel (Q 2^-e for the scores, Q x 2^9e and
-  // dO x 2^10e for the dK and dV products)
-  const bf16* Qx = XT ? static_cast<const bf16*>(p.qx) + (int64_t)bh * N * D : nullptr;
-  const bf16* dOx = XT ? static_cast<const bf16*>(p.dox) + (int64_t)bh * N * D : nullptr;
+  const float* RCg4 = rc_plane(p, bh, XT ? 6 : 7);
+  // XT: Q 2^-e, written by the dQ kernel
   const bf16* Qsc = XT ? static_cast<const bf16*>(p.qs) + (int64_t)bh * N * D : nullptr;
   // The workgroup's 64-key tiles.  With the tile activity of the dQ stage, workgroup j of a
   // (b, h) takes positions TPW j .. TPW j + TPW - 1 of the order "active tiles ascending, then
@@ -1446,7 +1421,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const bool live = has_keys && wact;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
-  const float ds_mult = 10.f * scale;  // XT: the score loops form dS/(10 scale x)
+  const float c_ds = 10.f * scale;  // XT: dS = (aw c) dw + tie
   const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
 
   bf16x8 kf[KB][KS], vf[KB][KS];
@@ -1490,22 +1465,20 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
 
   // Tiles go straight from global memory to LDS buffer bb; rows >= N repeat row N - 1 (their
   // scores are masked), including their row constants.  D <= 64: whole tiles take a scalar
-  // base plus the lanes' fixed 32-bit offsets (the scaled copies share one set: both have row
-  // stride D); D = 128, at the register limit, forms every address from the row and column.
-  const TileDma<D, DK> tq(w, lane, p.qsn), tdo(w, lane, p.dosn), tx(w, lane, D);
+  // base plus the lanes' fixed 32-bit offsets; D = 128, at the register limit, forms every
+  // address from the row and column.
+  const TileDma<D, DK> tq(w, lane, XT ? D : p.qsn), tdo(w, lane, p.dosn);
   auto load_tile = [&](int m, const QBuf& bb) {
     if (XT) {
-      tx.load(Qsc, D, m, N, bb.q, w);
+      tq.load(Qsc, D, m, N, bb.q, w);
       tdo.load(dO, p.dosn, m, N, bb.o, w);
-      tx.load(Qx, D, m, N, bb.qx, w);
-      tx.load(dOx, D, m, N, bb.ox, w);
     } else {
       tq.load_clamped(Q, p.qsn, m, N, bb.q, w);
       tq.load_clamped(dO, p.dosn, m, N, bb.o, w);
     }
     const int row = min(m + lane, N - 1);
-    if (w < NPL) lds_dma4(RCgw + row, bb.rc + w * BMQ);
-    if (!XT && w == 0) lds_dma4(RCg4 + row, bb.rc + (NPL - 1) * BMQ);
+    lds_dma4(RCgw + row, bb.rc + w * BMQ);
+    if (w == 0) lds_dma4(RCg4 + row, bb.rc + (NPL - 1) * BMQ);
   };
   if (qt0 < nqt) load_tile((nqt - 1) * BMQ, buf0);
 
@@ -1532,8 +1505,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     if (work) {
       const bf16* Qc = bc.q;
       const bf16* dOc = bc.o;
-      const bf16* Qt = XT ? bc.qx : Qc;    // operand of dK += dS^T Q
-      const bf16* dOt = XT ? bc.ox : dOc;  // operand of dV += w^T dO
+      const bf16* Qt = Qc;    // operand of dK += dS^T Q (XT: dS 2^e and Q 2^-e)
+      const bf16* dOt = dOc;  // operand of dV += w^T dO
       const bool masked = (CAUSAL && m0 < kw0 + KPW - 1) || m0 + BMQ > N || kw0 + KPW > N;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
@@ -1577,8 +1550,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         if (masked) mask_qk<KB>(s, m0, hf, kw0, N, CAUSAL, g, r16);
         // rows 32 hf + 8 g + 4 qq + (0..3) of the tile are perm_row(2 hf + qq, 4 g + i)
         if constexpr (XT) {
-          if (ties) w_ds_qk_x<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
-          else w_ds_qk_x_notie<KB>(s, dw);
+          if (ties) w_ds_qk_x<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g, c_ds);
+          else w_ds_qk_x_notie<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g, c_ds);
         } else {
           if (ties) w_ds_qk<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
           else w_ds_qk_notie<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
@@ -1620,7 +1593,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         bf16x4 k4, v4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          k4[i] = (bf16)(XT ? adk[db][kb][i] * ds_mult : adk[db][kb][i]);
+          k4[i] = (bf16)adk[db][kb][i];
           v4[i] = (bf16)adv[db][kb][i];
         }
         *reinterpret_cast<bf16x4*>(dK + (int64_t)key * p.dksn + 16 * db + 4 * g) = k4;

@@ -187,20 +187,18 @@ extern "C" int pnfx_flash_bwd_stages(int stages, const void* q, int64_t qsb, int
   char* ws = static_cast<char*>(workspace);
   float* rcbuf = reinterpret_cast<float*>(ws);
   double* parts = reinterpret_cast<double*>(ws + wl.rc_bytes);
-  void* qx = wl.xt_bytes ? ws + wl.rc_bytes + wl.parts_bytes : nullptr;
-  void* dox = wl.xt_bytes ? ws + wl.rc_bytes + wl.parts_bytes + wl.xt_bytes : nullptr;
-  void* qs = wl.xt_bytes ? ws + wl.rc_bytes + wl.parts_bytes + 2 * wl.xt_bytes : nullptr;
+  void* qs = wl.xt_bytes ? ws + wl.rc_bytes + wl.parts_bytes : nullptr;
   uint8_t* ktact = tile_mask ? reinterpret_cast<uint8_t*>(ws + wl.rc_bytes + wl.parts_bytes +
-                                                          3 * wl.xt_bytes)
+                                                          wl.xt_bytes)
                              : nullptr;
   uint8_t* amap = (tile_mask && wl.amap_bytes)
                       ? reinterpret_cast<uint8_t*>(ws + wl.rc_bytes + wl.parts_bytes +
-                                                   3 * wl.xt_bytes + wl.kt_bytes)
+                                                   wl.xt_bytes + wl.kt_bytes)
                       : nullptr;
   BwdParams bp{q, k, v, o, o_lo, dout, dq, dk, dv,
                qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, osb, osh, osn, dosb, dosh, dosn,
                dqsb, dqsh, dqsn, dksb, dksh, dksn, dvsb, dvsh, dvsn,
-               M, Z, tile_mask, rcbuf, parts, qx, dox, qs, ktact, amap, dtau,
+               M, Z, tile_mask, rcbuf, parts, qs, ktact, amap, dtau,
                (int)B, (int)H, (int)N, (int)((N + 31) / 32), (int)((N + 63) / 64),
                bwd_nkvb(N, D), tau, scale, gamma};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
