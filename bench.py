@@ -407,6 +407,43 @@ def bench_lm(dev, steps=10, warmup=3):
     return out
 
 
+def bench_host_overhead(dev, calls=400):
+    """Host time per call of the C++-registered ops (python -> dispatcher -> C ABI -> launch),
+    at a shape whose kernels take less GPU time than the host needs to enqueue them: the wall
+    time of a loop of calls with no synchronisation inside it (the launches queue up), over
+    the number of calls.  Forward alone (no grad), and a forward + backward through autograd."""
+    q, k, v = (torch.randn(1, 1, 64, 64, device=dev).to(torch.bfloat16) for _ in range(3))
+    tau = torch.zeros((), device=dev)
+    out = {"shape": [1, 1, 64, 64], "dtype": "bf16"}
+    flash = torch.ops.pnfx.flash_fwd
+
+    def fwd():
+        with torch.no_grad():
+            flash(q, k, v, tau, 0.125, 0.5, True, True, False, False)
+
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    tg = tau.clone().requires_grad_(True)
+    dO = torch.randn_like(q)
+
+    def fwd_bwd():
+        o = flash(qg, kg, vg, tg, 0.125, 0.5, True, True, False, False)[0]
+        torch.autograd.backward(o, dO)
+
+    for name, fn in (("flash_fwd_us_per_call", fwd), ("flash_fwd_bwd_us_per_step", fwd_bwd)):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                fn()
+            best = min(best, (time.perf_counter() - t0) / calls * 1e6)
+            torch.cuda.synchronize()
+        out[name] = round(best, 2)
+    return out
+
+
 MHA6 = dict(n_layers=6, d_model=64, n_heads=4, N=1024, B=16)
 
 
@@ -603,7 +640,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["flash", "flash_c5", "flash_silent", "fir", "fir_sweep", "fir_fused", "copy",
+    ap.add_argument("--only", choices=["flash", "flash_c5", "flash_silent", "fir", "fir_sweep", "fir_fused", "copy", "host",
                                        "lm", "mha6", "ref", "kernels", "rows"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -630,6 +667,9 @@ def main():
         return
     if args.only == "lm":
         print(json.dumps(bench_lm(dev)))
+        return
+    if args.only == "host":
+        print(json.dumps({"host_overhead": bench_host_overhead(dev)}))
         return
     if args.only == "mha6":
         print(json.dumps(bench_mha6(dev)))
@@ -723,6 +763,7 @@ def main():
     fir_fused = bench_fir_fused(dev)
     lm = bench_lm(dev)
     mha6 = bench_mha6(dev)
+    host = bench_host_overhead(dev)
     refcfg = bench_reference_configs(dev)
     rows = bench_rows(dev)
 
@@ -769,6 +810,7 @@ def main():
         "fir_fused_forward": fir_fused,
         "lm_step": lm,
         "mha6_stack": mha6,
+        "host_overhead": host,
         "reference_configs": refcfg,
         "row_kernels": rows,
         "cpu_baseline": cpu,

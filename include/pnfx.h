@@ -182,9 +182,10 @@ int pnfx_flash_bwd(const void* q, int64_t qsb, int64_t qsh, int64_t qsn, const v
  * The three stages of pnfx_flash_bwd, callable separately (same arguments,
  * plus a stage mask), and run in this order on one workspace: PNFX_BWD_PREPARE
  * forms the per-row constants (and clears the key-tile activity bytes);
- * PNFX_BWD_DQ writes dq and dtau, stores each row's peak-tie share G/Nmax and
- * marks the 64-key tiles with an active tile_mask entry; PNFX_BWD_DKDV (which
- * reads both) writes dk and dv.  pnfx_flash_bwd is the mask PNFX_BWD_ALL.
+ * PNFX_BWD_DQ writes dq and the tau partials, stores each row's peak-tie share
+ * and marks the 64-key tiles with an active tile_mask entry; PNFX_BWD_DKDV (which
+ * reads all of these) writes dk, dv and (bf16) dtau.  For fp32 the DQ stage writes
+ * dtau.  pnfx_flash_bwd is the mask PNFX_BWD_ALL.
  */
 #define PNFX_BWD_PREPARE 1
 #define PNFX_BWD_DKDV 2

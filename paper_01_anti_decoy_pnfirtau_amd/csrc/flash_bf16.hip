@@ -22,9 +22,9 @@
 //
 // Backward (deterministic, no atomics), in this order: a per-row preprocess kernel forms the
 // row constants (D_i = <dO_i, O_i>/g_i and the gate/normaliser factors); a query-parallel
-// kernel accumulates dQ and the tau partials and counts the peak ties; a one-block kernel
-// sums the partials in fp64; a key-parallel kernel accumulates dK and dV.  Both gradient
-// kernels skip the 32x64 sub-tiles that the forward recorded as silent.
+// kernel accumulates dQ and the tau partials and counts the peak ties; a key-parallel kernel
+// accumulates dK and dV, and one of its workgroups sums the tau partials in fp64.  Both
+// gradient kernels skip the 32x64 sub-tiles that the forward recorded as silent.
 #include <cmath>
 
 #include "flash.h"
@@ -1352,6 +1352,27 @@ __device__ __forceinline__ int ordered_ktile(const uint8_t* act, int nk64, int e
   return -1;
 }
 
+// dtau = -(sum of all du partials), summed in fp64 by one 256-thread workgroup in a fixed
+// order (deterministic); each thread keeps eight independent loads in flight.  Run by the
+// first workgroup of the dK/dV kernel after its own keys: the dQ stage that wrote the
+// partials has finished by then (stream order), no launch of its own is needed, and that
+// workgroup (the heaviest causal key block, dispatched first) ends well before the kernel.
+__device__ __forceinline__ void dtau_sum(const double* partials, int64_t n, float* dtau, int tid) {
+  __shared__ double red[4];
+  double a[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  int64_t i = tid;
+  for (; i + 7 * 256 < n; i += 8 * 256) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] += partials[i + u * 256];
+  }
+  for (; i < n; i += 256) a[0] += partials[i];
+  const double acc =
+      wave_sum_d(((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7])));
+  if ((tid & 63) == 0) red[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) dtau[0] = (float)(-((red[0] + red[1]) + (red[2] + red[3])));
+}
+
 template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   // D <= 64: the scores are peak-normalised per row (from the dQ kernel's copy Q 2^-e, which
@@ -1601,27 +1622,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
       }
     }
   }
-}
-
-// dtau = -(sum of all du partials), summed in fp64 by one block in a fixed order
-// (deterministic).  Each thread keeps four independent loads in flight.
-__global__ __launch_bounds__(1024) void flash_dtau_kernel(const double* partials, int64_t n,
-                                                          float* dtau) {
-  __shared__ double red[16];
-  const int tid = threadIdx.x;
-  double a[4] = {0.0, 0.0, 0.0, 0.0};
-  int64_t i = tid;
-  for (; i + 3 * 1024 < n; i += 4 * 1024) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) a[u] += partials[i + u * 1024];
-  }
-  for (; i < n; i += 1024) a[0] += partials[i];
-  double acc = wave_sum_d((a[0] + a[1]) + (a[2] + a[3]));
-  if ((tid & 63) == 0) red[tid >> 6] = acc;
-  __syncthreads();
-  if (tid < 64) {
-    acc = wave_sum_d(tid < 16 ? red[tid] : 0.0);
-    if (tid == 0) dtau[0] = (float)(-acc);
+  if (blockIdx.x == 0) {  // the dQ stage's tau partials (one per dQ wave)
+    constexpr int64_t rw = 64 * dq_qblocks(D);
+    dtau_sum(p.partials, (int64_t)p.B * p.H * ((p.N + rw - 1) / rw) * 4, p.dtau, tid);
   }
 }
 
@@ -1702,12 +1705,10 @@ int launch_bwd_d(const BwdParams& bp_in, bool causal, bool has_gamma, int stages
     const dim3 gdq((unsigned)(nqb * bp.B * bp.H));
     if (ps) launch_dq<D, true>(bp, causal, gdq, st);
     else launch_dq<D, false>(bp, causal, gdq, st);
-    hipLaunchKernelGGL(flash_dtau_kernel, dim3(1), dim3(1024), 0, st, bp.partials,
-                       (int64_t)bp.B * bp.H * nqb * 4, bp.dtau);
     const int rc = launch_status("pnfx_flash_bwd(dq)");
     if (rc) return rc;
   }
-  if (stages & PNFX_BWD_DKDV) {  // reads the G/Nmax the dQ stage wrote
+  if (stages & PNFX_BWD_DKDV) {  // reads the tie terms and tau partials the dQ stage wrote
     const dim3 gkv((unsigned)(bp.nkvb * bp.B * bp.H));
     if (causal) {
       if (ps) hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, true, true>), gkv, block, 0, st, bp);

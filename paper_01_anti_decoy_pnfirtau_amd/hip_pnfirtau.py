@@ -45,7 +45,7 @@ def hip_causal_fir(x: torch.Tensor, taps: torch.Tensor) -> torch.Tensor:
     (src/triton_pnfirtau.py:685-691): CPU tensors, other tap counts, wider rows.
     """
     if x.is_cuda and taps.numel() == FIR_KERNEL_TAPS and x.shape[-1] <= FIR_KERNEL_MAX_C:
-        return torch.ops.pnfx.fir_fwd(x, taps.reshape(-1))
+        return torch.ops.pnfx.fir_fwd.default(x, taps.reshape(-1))
     return causal_fir(x, taps)
 
 
@@ -53,7 +53,7 @@ def hip_causal_fir_heads(k: torch.Tensor, taps: torch.Tensor) -> torch.Tensor:
     """Causal FIR along N of keys in [B, H, N, d] layout with per-head taps [H, K] (or shared [K])."""
     if not k.is_cuda:
         raise RuntimeError("hip_causal_fir_heads runs on the GPU only")
-    return torch.ops.pnfx.fir_fwd(k, taps)
+    return torch.ops.pnfx.fir_fwd.default(k, taps)
 
 
 def hip_pn_fir_tau_scores(
@@ -79,7 +79,7 @@ def hip_pn_fir_tau_scores(
     N = raw_scores.shape[-1]
     assert raw_scores.shape[-2] == N, "Expected [..., N, N] scores tensor"
     has_gamma = gamma is not None and gamma > 0.0
-    w, _, _, _ = torch.ops.pnfx.pn_rows_fwd(raw_scores, score_tau, float(scale), float(p),
+    w, _, _, _ = torch.ops.pnfx.pn_rows_fwd.default(raw_scores, score_tau, float(scale), float(p),
                                             float(gamma) if has_gamma else 0.0, has_gamma,
                                             bool(causal_mask))
     return w
@@ -93,7 +93,7 @@ def _flash_attention(q, k, v, score_tau, scale, gamma, causal_mask, o_bnhd=False
     k = k if k.dtype == q.dtype else k.to(q.dtype)
     v = v if v.dtype == q.dtype else v.to(q.dtype)
     has_gamma = gamma is not None and gamma > 0.0
-    o = torch.ops.pnfx.flash_fwd(q, k, v, score_tau, float(scale),
+    o = torch.ops.pnfx.flash_fwd.default(q, k, v, score_tau, float(scale),
                                  float(gamma) if has_gamma else 0.0, has_gamma,
                                  bool(causal_mask), bool(o_bnhd), False)[0]
     return o
@@ -123,21 +123,20 @@ def flash_pn_fir_tau_attention_with_stats(q, k_tilde, v, score_tau, scale=None, 
                                           causal_mask=True):
     """Forward only: (O, M, Z, Nmax, tile_mask) -- the saved statistics and the silence map.
 
-    M is the row peak of u = relu(q k^T scale - tau), Nmax its tie count.  Z is the
-    normaliser O is divided by: the sum of P = u^10 plus 1e-12.  For bf16 inputs P is
-    rounded to bf16 before it weights V (as the reference's kernel does,
-    src/triton_pnfirtau.py:417-420), and Z sums exactly those rounded values -- so O is a
-    convex combination of the rows of V scaled by the gate; the reference's kernel sums the
-    unrounded fp32 P instead (:405, :422), which differs from this Z by the rounding of
-    the P terms (a relative 2^-8 at most, and far less on rows with many comparable
-    terms).  For fp32 inputs both sum the fp32 P.
+    M is the row peak of u = relu(q k^T scale - tau), Nmax its tie count, and Z the
+    reference's normaliser: the sum of P = u^10 (unrounded fp32) plus 1e-12
+    (src/triton_pnfirtau.py:405, :422).  For bf16 inputs P is rounded to bf16 before it
+    weights V (as the reference's kernel does, :417-420), and O is divided by the sum of
+    exactly those rounded values, so that it is a convex combination of the rows of V scaled
+    by the gate (the reference divides by Z; the two normalisers differ by the rounding of
+    the P terms, a relative 2^-8 at most).  For fp32 inputs both are the fp32 sum.
     """
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     has_gamma = gamma is not None and gamma > 0.0
     k_tilde = k_tilde if k_tilde.dtype == q.dtype else k_tilde.to(q.dtype)
     v = v if v.dtype == q.dtype else v.to(q.dtype)
-    o, _, M, Z, Nm, mask = torch.ops.pnfx.flash_fwd(q, k_tilde, v, score_tau, float(scale),
+    o, _, M, Z, Nm, mask = torch.ops.pnfx.flash_fwd.default(q, k_tilde, v, score_tau, float(scale),
                                                    float(gamma) if has_gamma else 0.0, has_gamma,
                                                    bool(causal_mask), False, True)
     return o, M, Z, Nm, mask
