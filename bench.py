@@ -278,30 +278,89 @@ def bench_fir_sweep(dev):
     return out
 
 
-def bench_fir_fused(dev, steps=20, warmup=5):
-    """Forward only (inference) at C4 with raw keys: the causal FIR then the flash forward
-    (two launches, src/pnfirtau_attention.py:299-315) against the forward with the FIR fused
-    into its key-tile load (pnfx_flash_fwd_fir).  The outputs are bitwise equal
-    (tests/test_gpu_fused_fir.py)."""
+def _graph_ms(fn, reps=20, replays=10):
+    """GPU time per call of fn from one HIP graph of `reps` calls, replayed `replays` times
+    (no host launch cost in it)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        g.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / (replays * reps) * 1e3
+
+
+STACK_INF = dict(n_layers=6, d_model=64, n_heads=4, N=256, B=64)
+FUSED_FIR_SHAPES = [  # B, H, N, D: the mha6 stack, kern1 (N = 256), the C3 attention, C4
+    (16, 4, 1024, 16), (64, 4, 256, 16), (32, 4, 512, 64), (4, 16, 8192, 64)]
+
+
+def bench_fir_fused(dev, steps=30, warmup=5):
+    """Forward only (inference) with raw keys: the causal FIR then the flash forward (two
+    launches, src/pnfirtau_attention.py:299-315) against the forward with the FIR fused into
+    its key-tile load (pnfx_flash_fwd_fir), bitwise equal outputs
+    (tests/test_gpu_fused_fir.py).  Per shape: eager wall time per call between
+    synchronisations (host launch cost included) and GPU time per call from a replayed HIP
+    graph; then a stack of 6 PnFirTauFlashMHA layers at the kern1 shape (d = 16, N = 256) in
+    inference, eager and as a graph, with the module's fused route on and off."""
+    from paper_01_anti_decoy_pnfirtau_amd import PnFirConfig, PnFirTauFlashMHA, hip_pnfirtau
     from paper_01_anti_decoy_pnfirtau_amd import ops
     from paper_01_anti_decoy_pnfirtau_amd.pnfirtau_attention import causal_gaussian_taps
 
-    B, H, N, D = C4["B"], C4["H"], C4["N"], C4["D"]
-    q, kraw, v, _ = make_inputs(B, H, N, D, 3, dev)
+    out = {"shapes": []}
     taps = causal_gaussian_taps(7).to(dev)
     t32 = torch.tensor(0.0, device=dev)
+    for B, H, N, D in FUSED_FIR_SHAPES:
+        q, kraw, v, _ = make_inputs(B, H, N, D, 3, dev)
 
-    def two():
-        k = torch.ops.pnfx.fir_fwd(kraw, taps)
-        torch.ops.pnfx.flash_fwd(q, k, v, t32, D ** -0.5, 0.5, True, True, False, False)
+        def two():
+            k = torch.ops.pnfx.fir_fwd.default(kraw, taps)
+            torch.ops.pnfx.flash_fwd.default(q, k, v, t32, D ** -0.5, 0.5, True, True, False, False)
 
-    def fused():
-        ops.flash_fwd_fused_fir(q, kraw, v, t32, taps, D ** -0.5, 0.5, True, True)
+        def fused():
+            ops.flash_fwd_fused_fir(q, kraw, v, t32, taps, D ** -0.5, 0.5, True, True)
 
-    w2, e2 = time_steps(two, steps, warmup)
-    wf, ef = time_steps(fused, steps, warmup)
-    return {"config": "C4 forward, raw keys, tau = 0", "fir_then_flash_ms": round(e2, 4),
-            "fused_fir_flash_ms": round(ef, 4), "fused_over_two_launches": round(ef / e2, 3)}
+        w2, _ = time_steps(two, steps, warmup)
+        wf, _ = time_steps(fused, steps, warmup)
+        g2, gf = _graph_ms(two), _graph_ms(fused)
+        out["shapes"].append({"B": B, "H": H, "N": N, "D": D,
+                              "eager_ms": {"fir_then_flash": round(w2, 4), "fused": round(wf, 4)},
+                              "graph_ms": {"fir_then_flash": round(g2, 4), "fused": round(gf, 4)},
+                              "fused_over_two_launches_gpu": round(gf / g2, 3)})
+        del q, kraw, v
+    torch.manual_seed(42)
+    acfg = PnFirConfig(d_model=STACK_INF["d_model"], n_heads=STACK_INF["n_heads"])
+    layers = torch.nn.ModuleList(
+        [PnFirTauFlashMHA(acfg) for _ in range(STACK_INF["n_layers"])]).to(dev)
+    x = torch.randn(STACK_INF["B"], STACK_INF["N"], STACK_INF["d_model"], device=dev,
+                    dtype=torch.bfloat16)
+
+    def stack():
+        with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            h = x
+            for lyr in layers:
+                h = h + lyr(h)
+        return h
+
+    res = {}
+    for route in (False, True):
+        hip_pnfirtau.FUSED_FIR_INFERENCE = route
+        wall, _ = time_steps(stack, steps, warmup)
+        res["fused" if route else "fir_then_flash"] = {"eager_ms": round(wall, 4),
+                                                        "graph_ms": round(_graph_ms(stack, 1, 20), 4)}
+    hip_pnfirtau.FUSED_FIR_INFERENCE = True
+    out["stack_inference"] = {"config": STACK_INF, "tau": 0.0, **res}
+    return out
 
 
 def bench_rows(dev, reps=20):

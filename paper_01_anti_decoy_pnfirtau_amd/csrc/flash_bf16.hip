@@ -382,7 +382,7 @@ __device__ __forceinline__ float max_nonneg(float a, float b) {
 constexpr int kMaxListTiles = 1024;
 
 // COUNT: also count the peak ties (Nmax); the training path leaves that to the backward.
-// FIRK (D = 64 only): p.k holds the raw keys, and each key tile is filtered in LDS (the causal
+// FIRK (D <= 64): p.k holds the raw keys, and each key tile is filtered in LDS (the causal
 // FIR of pnfx_fir_fwd, fused into the key-tile load) before its scores; see
 // pnfx_flash_fwd_fir.
 template <int D, bool CAUSAL, bool PS, bool COUNT, bool FIRK = false>
@@ -392,17 +392,18 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
   constexpr int DK = D < 32 ? 32 : D;
   constexpr int KS = DK / 32;
   constexpr int DB = D / 16;
-  static_assert(!FIRK || D == 64, "the fused FIR is built for d = 64");
+  static_assert(!FIRK || D <= 64, "the fused FIR is built for d <= 64");
   // Two K/V tile buffers as separate LDS objects (see the dK/dV kernel), filled straight
   // from global memory.
   __shared__ __attribute__((aligned(16))) bf16 Ks0[BN * DK];
   __shared__ __attribute__((aligned(16))) bf16 Vs0[BN * DK];
   __shared__ __attribute__((aligned(16))) bf16 Ks1[BN * DK];
   __shared__ __attribute__((aligned(16))) bf16 Vs1[BN * DK];
-  // FIRK: the raw key rows n0 - 8 .. n0 + 63 of each tile, row-major [72][64]
+  // FIRK: the raw key rows n0 - 8 .. n0 + 63 of each tile, row-major [72][D]
   constexpr int KR_ROWS = 72;
-  __shared__ __attribute__((aligned(16))) bf16 Kr0[FIRK ? KR_ROWS * DK : 8];
-  __shared__ __attribute__((aligned(16))) bf16 Kr1[FIRK ? KR_ROWS * DK : 8];
+  constexpr int KCPR = D / 8;  // 16-byte chunks per raw key row
+  __shared__ __attribute__((aligned(16))) bf16 Kr0[FIRK ? KR_ROWS * D : 8];
+  __shared__ __attribute__((aligned(16))) bf16 Kr1[FIRK ? KR_ROWS * D : 8];
   const KVBuf buf0{Ks0, Vs0, Kr0}, buf1{Ks1, Vs1, Kr1};
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r16 = lane & 15;
@@ -533,15 +534,20 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
   const TileDma<D, DK> kdma(w, lane, p.ksn), vdma(w, lane, p.vsn);
   auto load_tile = [&](int n, const KVBuf& bb) {
     if constexpr (FIRK) {
-      // raw rows n - 8 .. n + 63, 8 chunks each (576 chunks: two per lane, a third for wave 0);
+      // raw rows n - 8 .. n + 63, KCPR chunks each (72 KCPR chunks, 64 per wave and load);
       // rows outside [0, N) re-load a real row (the filter skips rows before 0, and keys past
       // N are masked)
 #pragma unroll
-      for (int j = 0; j < 3; ++j) {
-        if (j == 2 && w != 0) break;
-        const int L = j * 256 + w * 64 + lane;
-        const int r = min(max(n - 8 + (L >> 3), 0), N - 1);
-        lds_dma16(K + (int64_t)r * p.ksn + 8 * (L & 7), bb.kr + (j * 256 + w * 64) * 8);
+      for (int j = 0; j < (KR_ROWS * KCPR + 255) / 256; ++j) {
+        const int L0 = j * 256 + w * 64;  // wave-uniform
+        if (L0 >= KR_ROWS * KCPR) break;
+        // each active lane lands 16 bytes at (its wave's base) + 16 lane: lanes past the last
+        // chunk stay inactive, so nothing lands beyond the buffer
+        const int L = L0 + lane;
+        if (L < KR_ROWS * KCPR) {
+          const int r = min(max(n - 8 + L / KCPR, 0), N - 1);
+          lds_dma16(K + (int64_t)r * p.ksn + 8 * (L % KCPR), bb.kr + L0 * 8);
+        }
       }
     } else {
       kdma.load(K, p.ksn, n, N, bb.k, w);
@@ -557,18 +563,23 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
   }
   // FIRK: the filtered key tile n0 .. n0 + 63 formed in bc.k from the raw rows in bc.kr, with
   // pnfx_fir_fwd's arithmetic (an fp32 FMA chain in lag order, one bf16 rounding): thread tid
-  // forms rows r0, r0 + 1 (r0 = 2 (tid / 8)) of chunk tid % 8.
+  // forms FRT consecutive rows from r0 = FRT (tid / KCPR) of chunk tid % KCPR (two rows at
+  // D = 64, one at D = 32; at D = 16 the first 128 threads one row each).
+  constexpr int FRT = KCPR >= 8 ? 2 : 1;
+  constexpr int FTHREADS = 64 * KCPR / FRT;
   auto filter_tile = [&](int n0, const KVBuf& bc) {
-    const int c = tid & 7, r0 = 2 * (tid >> 3);
-    u32x4 x[8];  // raw rows n0 + r0 - 6 .. n0 + r0 + 1
+    if (tid >= FTHREADS) return;
+    const int c = tid % KCPR, r0 = FRT * (tid / KCPR);
+    u32x4 x[FRT + 6];  // raw rows n0 + r0 - 6 .. n0 + r0 + FRT - 1
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = *reinterpret_cast<const u32x4*>(bc.kr + (r0 + 2 + i) * DK + 8 * c);
+    for (int i = 0; i < FRT + 6; ++i)
+      x[i] = *reinterpret_cast<const u32x4*>(bc.kr + (r0 + 2 + i) * D + 8 * c);
     const auto elem = [](const u32x4& v, int e) {
       const uint32_t d = v[e >> 1];
       return __uint_as_float((e & 1) ? (d & 0xffff0000u) : (d << 16));
     };
 #pragma unroll
-    for (int o = 0; o < 2; ++o) {
+    for (int o = 0; o < FRT; ++o) {
       const int n = n0 + r0 + o;
       float acc[8];
 #pragma unroll
@@ -584,6 +595,16 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
       *reinterpret_cast<bf16x8*>(bc.k + rt_off<DK>(r0 + o, c)) = y;
     }
   };
+  // FIRK, D < DK (D = 16): the K tiles' padding chunks meet only zero Q fragments but must hold
+  // finite values; the filter never writes them, so they are zeroed once here (published by
+  // the first tile's barrier).
+  if constexpr (FIRK && D < DK) {
+    for (int i = tid; i < 2 * 64 * (DK - D) / 8; i += 256) {
+      const int bsel = i / (64 * (DK - D) / 8), j = i % (64 * (DK - D) / 8);
+      const int row = j / ((DK - D) / 8), c = KCPR + j % ((DK - D) / 8);
+      *reinterpret_cast<bf16x8*>((bsel ? buf1.k : buf0.k) + rt_off<DK>(row, c)) = zero_bf16x8();
+    }
+  }
   // Entry e of the list: tile t, computed from buffer bc while the next entry's tile tn
   // streams into buffer bn.
   auto step = [&](int e, const KVBuf& bc, const KVBuf& bn) {
@@ -1655,16 +1676,17 @@ void launch_fwd_dp(const FwdParams& fp, bool causal, hipStream_t st) {
   }
 }
 
+template <int D>
 int flash_fwd_fir_launch(const FwdParams& fp, bool causal, hipStream_t st) {
   const int nqb = (fp.N + 127) / 128;
   const dim3 grid((unsigned)(nqb * fp.B * fp.H)), block(256);
   const bool ps = pow2_scale(fp.scale);
   if (causal) {
-    if (ps) hipLaunchKernelGGL((flash_fwd_kernel<64, true, true, false, true>), grid, block, 0, st, fp);
-    else hipLaunchKernelGGL((flash_fwd_kernel<64, true, false, false, true>), grid, block, 0, st, fp);
+    if (ps) hipLaunchKernelGGL((flash_fwd_kernel<D, true, true, false, true>), grid, block, 0, st, fp);
+    else hipLaunchKernelGGL((flash_fwd_kernel<D, true, false, false, true>), grid, block, 0, st, fp);
   } else {
-    if (ps) hipLaunchKernelGGL((flash_fwd_kernel<64, false, true, false, true>), grid, block, 0, st, fp);
-    else hipLaunchKernelGGL((flash_fwd_kernel<64, false, false, false, true>), grid, block, 0, st, fp);
+    if (ps) hipLaunchKernelGGL((flash_fwd_kernel<D, false, true, false, true>), grid, block, 0, st, fp);
+    else hipLaunchKernelGGL((flash_fwd_kernel<D, false, false, false, true>), grid, block, 0, st, fp);
   }
   return launch_status("pnfx_flash_fwd_fir");
 }
@@ -1739,11 +1761,13 @@ int flash_fwd_bf16(const FwdParams& fp, int64_t D, bool causal, hipStream_t st) 
 }
 
 int flash_fwd_fir_bf16(const FwdParams& fp, int64_t D, bool causal, hipStream_t st) {
-  if (D != 64) {
-    set_error("flash_fwd_fir: head dim %lld (the fused FIR is built for 64)", (long long)D);
-    return PNFX_EUNSUPPORTED;
+  switch (D) {
+    case 16: return flash_fwd_fir_launch<16>(fp, causal, st);
+    case 32: return flash_fwd_fir_launch<32>(fp, causal, st);
+    case 64: return flash_fwd_fir_launch<64>(fp, causal, st);
   }
-  return flash_fwd_fir_launch(fp, causal, st);
+  set_error("flash_fwd_fir: head dim %lld (the fused FIR is built for 16, 32, 64)", (long long)D);
+  return PNFX_EUNSUPPORTED;
 }
 
 int flash_bwd_bf16(const BwdParams& bp, int64_t D, bool causal, bool has_gamma, int stages,

@@ -267,14 +267,14 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> flash_bwd_cuda(
 
 std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> flash_fwd_fir_cuda(
     const Tensor& q_in, const Tensor& kraw_in, const Tensor& v_in, const Tensor& tau,
-    const Tensor& taps, double scale, double gamma, bool has_gamma, bool causal) {
+    const Tensor& taps, double scale, double gamma, bool has_gamma, bool causal, bool o_bnhd) {
   check_qkv(q_in, kraw_in, v_in);
   const int code = dtype_code(q_in, "flash_fwd_fir");
   const Tensor q = bhnd(q_in, "q", true), kr = bhnd(kraw_in, "k_raw", true),
                v = bhnd(v_in, "v", true);
   const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
   const Tensor taps2 = taps.reshape({-1, taps.size(-1)}).to(q.device(), at::kFloat).contiguous();
-  auto [o, o_lo] = new_o_pair(q, false, true);
+  auto [o, o_lo] = new_o_pair(q, o_bnhd, true);
   Tensor stats = at::empty({2, B, H, N}, q.options().dtype(at::kFloat));
   Tensor M = stats[0], Z = stats[1];
   const auto ms = mask_shape(B, H, N);
@@ -433,7 +433,8 @@ TORCH_LIBRARY(pnfx, m) {
         "Tensor M, Tensor Z, Tensor mask, float scale, float gamma, bool has_gamma, bool causal) "
         "-> (Tensor, Tensor, Tensor, Tensor)");
   m.def("flash_fwd_fir(Tensor q, Tensor k_raw, Tensor v, Tensor tau, Tensor taps, float scale, "
-        "float gamma, bool has_gamma, bool causal) -> (Tensor, Tensor, Tensor, Tensor, Tensor)");
+        "float gamma, bool has_gamma, bool causal, bool o_bnhd=False) -> "
+        "(Tensor, Tensor, Tensor, Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(pnfx, CUDA, m) {

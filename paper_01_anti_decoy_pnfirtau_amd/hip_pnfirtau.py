@@ -99,6 +99,45 @@ def _flash_attention(q, k, v, score_tau, scale, gamma, causal_mask, o_bnhd=False
     return o
 
 
+# PnFirTauFlashMHA's inference forward (no autograd) runs the key FIR inside the flash
+# forward's key-tile load when this is set and fused_fir_forward_applies(); False keeps the two
+# launches (FIR, then flash) everywhere.
+FUSED_FIR_INFERENCE = True
+# The fused forward filters each key tile once per 128-query block that reads it, so its extra
+# work grows with N while the launch it saves does not.  Measured on MI355X (GPU time per
+# forward, from replayed HIP graphs): 0.80x the two launches at B=64 H=4 N=256 d=16, 0.95x at
+# B=32 H=4 N=512 d=64, 1.04x at B=16 H=4 N=1024 d=16 and 1.64x at B=4 H=16 N=8192 d=64.
+FUSED_FIR_MAX_N = 512
+
+
+def fused_fir_forward_applies(q: torch.Tensor, k_raw: torch.Tensor, taps: torch.Tensor,
+                              head_dim: int) -> bool:
+    """Whether the module's forward may take the fused FIR + flash forward: inference (no
+    tensor needs a gradient), bf16 GPU tensors, the reference's 7-tap kernel path of
+    hip_causal_fir (src/triton_pnfirtau.py:687: K == 7, at most 1024 channels), a head size
+    the fused kernel covers and a sequence where it measures faster (N <= FUSED_FIR_MAX_N).
+    k_raw is [B, N, D]."""
+    if not (FUSED_FIR_INFERENCE and q.is_cuda and q.dtype == torch.bfloat16
+            and k_raw.dtype == torch.bfloat16 and head_dim in (16, 32, 64)
+            and k_raw.shape[-2] <= FUSED_FIR_MAX_N
+            and taps.numel() == FIR_KERNEL_TAPS and k_raw.shape[-1] <= FIR_KERNEL_MAX_C):
+        return False
+    return not (torch.is_grad_enabled() and (q.requires_grad or k_raw.requires_grad
+                                              or taps.requires_grad))
+
+
+def fused_fir_flash_forward(q, k_raw, v, taps, score_tau, scale, gamma, causal_mask):
+    """O [B, H, N, d] (backed by [B, N, H, d] memory) of the flash forward with the causal FIR of
+    the raw keys fused into its key-tile load: bitwise hip_causal_fir followed by
+    flash_pn_fir_tau_attention (src/pnfirtau_attention.py:299-315) for the inputs
+    fused_fir_forward_applies() accepts.  No autograd."""
+    v = v if v.dtype == q.dtype else v.to(q.dtype)
+    has_gamma = gamma is not None and gamma > 0.0
+    return torch.ops.pnfx.flash_fwd_fir.default(q, k_raw, v, score_tau, taps.reshape(-1),
+                                                float(scale), float(gamma) if has_gamma else 0.0,
+                                                has_gamma, bool(causal_mask), True)[0]
+
+
 def flash_pn_fir_tau_attention(
     q: torch.Tensor,
     k_tilde: torch.Tensor,

@@ -83,14 +83,15 @@ def _new_o(q: Tensor, o_bnhd: bool) -> Tensor:
 
 
 def flash_fwd_fused_fir(q: Tensor, k_raw: Tensor, v: Tensor, tau: Tensor, taps: Tensor,
-                        scale: float, gamma: float, has_gamma: bool,
-                        causal: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+                        scale: float, gamma: float, has_gamma: bool, causal: bool,
+                        o_bnhd: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Flash forward with the causal FIR of the keys fused into the key-tile load
     (pnfx::flash_fwd_fir): k_raw are the keys before the FIR, taps as fir_fwd (fp32 [K] or
     [H, K], K <= 7).  Returns (O, O_lo, M, Z, tile_mask), bitwise those of fir_fwd followed by
-    flash_fwd.  bf16, inference only (no autograd, no tie counts): the filtered keys are not
-    materialised, so there is nothing for a backward to read."""
-    return torch.ops.pnfx.flash_fwd_fir(q, k_raw, v, tau, taps, scale, gamma, has_gamma, causal)
+    flash_fwd.  bf16, d in {16, 32, 64}, inference only (no autograd, no tie counts): the
+    filtered keys are not materialised, so there is nothing for a backward to read."""
+    return torch.ops.pnfx.flash_fwd_fir.default(q, k_raw, v, tau, taps, scale, gamma, has_gamma,
+                                                causal, o_bnhd)
 
 
 # ---------------------------------------------------------------------------- fake kernels
@@ -141,9 +142,9 @@ def _(q, k, v, tau, o, o_lo, do, M, Z, mask, scale, gamma, has_gamma, causal):
 
 
 @torch.library.register_fake("pnfx::flash_fwd_fir")
-def _(q, k_raw, v, tau, taps, scale, gamma, has_gamma, causal):
+def _(q, k_raw, v, tau, taps, scale, gamma, has_gamma, causal, o_bnhd=False):
     _check_qkv(q, k_raw, v)
     B, H, N, D = q.shape
     f = lambda: q.new_empty((B, H, N), dtype=torch.float32)  # noqa: E731
-    return (_new_o(q, False), _new_o(q, False), f(), f(),
+    return (_new_o(q, o_bnhd), _new_o(q, o_bnhd), f(), f(),
             q.new_empty(_mask_shape(B, H, N), dtype=torch.uint8))

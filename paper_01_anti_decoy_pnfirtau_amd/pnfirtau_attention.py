@@ -196,13 +196,20 @@ class PnFirTauFlashMHA(PnFirTauMHA):
     def forward(self, x: torch.Tensor, return_weights: bool = False):
         if return_weights:
             return PnFirTauTritonMHA.forward(self, x, return_weights=True)
-        from .hip_pnfirtau import _flash_attention, hip_causal_fir
+        from . import hip_pnfirtau as hp
 
         cfg = self.cfg
         B, N, D = x.shape
         q, k_raw, v = self.qkv(x).split(D, dim=-1)
-        k = self._split_heads(hip_causal_fir(k_raw, self.fir_taps))
+        if hp.fused_fir_forward_applies(q, k_raw, self.fir_taps, self.head_dim):
+            # inference: the key FIR inside the forward's key-tile load (one launch, same bits)
+            o = hp.fused_fir_flash_forward(self._split_heads(q), self._split_heads(k_raw),
+                                           self._split_heads(v), self.fir_taps, self.score_tau,
+                                           1.0 / math.sqrt(self.head_dim), cfg.silence_gamma,
+                                           cfg.causal_mask)
+            return self.out(o.transpose(1, 2).reshape(B, N, D))
+        k = self._split_heads(hp.hip_causal_fir(k_raw, self.fir_taps))
         q, v = self._split_heads(q), self._split_heads(v)
-        o = _flash_attention(q, k, v, self.score_tau, 1.0 / math.sqrt(self.head_dim),
-                             cfg.silence_gamma, cfg.causal_mask, o_bnhd=True)
+        o = hp._flash_attention(q, k, v, self.score_tau, 1.0 / math.sqrt(self.head_dim),
+                                cfg.silence_gamma, cfg.causal_mask, o_bnhd=True)
         return self.out(o.transpose(1, 2).reshape(B, N, D))
