@@ -174,6 +174,21 @@ std::pair<Tensor, Tensor> new_o_pair(const Tensor& q, bool o_bnhd, bool with_lo)
 
 const void* ptr_or_null(const Tensor& t) { return t.numel() ? t.data_ptr() : nullptr; }
 
+// Head sizes with a kernel of their own; any other size up to 128 is zero-padded to the next
+// one (as the reference pads D to BLOCK_D = next_pow2(max(D, 16)) with masked loads,
+// src/triton_pnfirtau.py:839-841): zero columns add exact zeros to every dot product, so the
+// scores, O and the gradients' real columns are those of the unpadded problem.
+bool kernel_head_dim(int64_t D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+int64_t padded_head_dim(int64_t D) { return D <= 16 ? 16 : D <= 32 ? 32 : D <= 64 ? 64 : 128; }
+Tensor pad_d(const Tensor& t, int64_t Dp) {
+  return t.numel() ? at::constant_pad_nd(t, {0, Dp - t.size(-1)}) : t;
+}
+void check_head_dim(int64_t D) {
+  TORCH_CHECK_VALUE(D >= 1 && D <= 128, "flash: head dim ", D,
+                    " has no flash kernel (1..128; flash_pn_fir_tau_attention and "
+                    "PnFirTauFlashMHA take the materialised-score path above 128)");
+}
+
 // A problem this small spends less time in the forward than the key-norm pass of the
 // silent-tile bound costs to launch: below it the forward runs without the bound (same results).
 constexpr int64_t kBoundMinScores = int64_t(1) << 26;  // B*H*N^2, e.g. B*H = 64 at N = 1024
@@ -186,6 +201,19 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> flash_fwd_cuda(
   check_qkv(q_in, k_in, v_in);
   const int code = dtype_code(q_in, "flash");
   const bool bf = code == PNFX_BF16;
+  TORCH_CHECK_VALUE(q_in.dim() == 4, "q must be [B,H,N,D], got ", q_in.sizes());
+  if (!kernel_head_dim(q_in.size(3))) {
+    const int64_t D = q_in.size(3);
+    check_head_dim(D);
+    const int64_t Dp = padded_head_dim(D);
+    auto [o, o_lo, M, Z, Nm, mask] = flash_fwd_cuda(pad_d(q_in, Dp), pad_d(k_in, Dp),
+                                                    pad_d(v_in, Dp), tau, scale, gamma, has_gamma,
+                                                    causal, false, with_nmax);
+    auto [oo, oo_lo] = new_o_pair(q_in, o_bnhd, bf);
+    oo.copy_(o.narrow(3, 0, D));
+    if (bf) oo_lo.copy_(o_lo.narrow(3, 0, D));
+    return {oo, oo_lo, M, Z, Nm, mask};
+  }
   const Tensor q = bhnd(q_in, "q", bf), k = bhnd(k_in, "k", bf), v = bhnd(v_in, "v", bf);
   const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
   auto [o, o_lo] = new_o_pair(q, o_bnhd, bf);
@@ -230,6 +258,18 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> flash_bwd_cuda(
                     q_in.sizes());
   const int code = dtype_code(q_in, "flash");
   const bool bf = code == PNFX_BF16;
+  TORCH_CHECK_VALUE(q_in.dim() == 4, "q must be [B,H,N,D], got ", q_in.sizes());
+  if (!kernel_head_dim(q_in.size(3))) {
+    const int64_t D = q_in.size(3);
+    check_head_dim(D);
+    const int64_t Dp = padded_head_dim(D);
+    auto [dq, dk, dv, dt] = flash_bwd_cuda(
+        pad_d(q_in, Dp), pad_d(k_in, Dp), pad_d(v_in, Dp), tau, pad_d(o_in, Dp),
+        o_lo.numel() == o_in.numel() ? pad_d(o_lo, Dp) : o_lo, pad_d(do_in, Dp), M, Z, mask,
+        scale, gamma, has_gamma, causal);
+    return {dq.narrow(3, 0, D).contiguous(), dk.narrow(3, 0, D).contiguous(),
+            dv.narrow(3, 0, D).contiguous(), dt};
+  }
   const Tensor q = bhnd(q_in, "q", bf), k = bhnd(k_in, "k", bf), v = bhnd(v_in, "v", bf);
   const Tensor o = bhnd(o_in, "o", bf);
   // the residual is used only with exactly O's layout (the C ABI takes one set of strides)

@@ -85,6 +85,26 @@ def hip_pn_fir_tau_scores(
     return w
 
 
+# Head sizes up to this have flash kernels (16, 32, 64, 128, the others zero-padded to the next
+# one inside the ops); larger heads take _materialised_attention.
+FLASH_MAX_HEAD_DIM = 128
+
+
+def _materialised_attention(q, k, v, score_tau, scale, gamma, causal_mask):
+    """pn_fir_tau attention for head sizes above FLASH_MAX_HEAD_DIM: the [B, H, N, N] scores in
+    fp32 (the reference's kernels accumulate q k^T in fp32 too), the HIP row-fused score kernel
+    in fp32 (pnfx::pn_rows_fwd, p = 10 and the peak gate) and W V in fp32, with autograd
+    through all three.  The same values as the flash path (src/triton_pnfirtau.py:313-621) at
+    O(N^2) memory -- the reference's flash kernel covers any head size by padding it to a power
+    of two (:839-841), which this GPU's flash kernels stop at 128."""
+    has_gamma = gamma is not None and gamma > 0.0
+    raw = torch.matmul(q.float(), k.float().transpose(-2, -1))
+    w = torch.ops.pnfx.pn_rows_fwd.default(raw, score_tau, float(scale), 10.0,
+                                           float(gamma) if has_gamma else 0.0, has_gamma,
+                                           bool(causal_mask))[0]
+    return torch.matmul(w, v.float()).to(q.dtype)
+
+
 def _flash_attention(q, k, v, score_tau, scale, gamma, causal_mask, o_bnhd=False):
     if not q.is_cuda:
         raise RuntimeError("flash_pn_fir_tau_attention runs on the GPU only (as in the reference)")
@@ -92,6 +112,8 @@ def _flash_attention(q, k, v, score_tau, scale, gamma, causal_mask, o_bnhd=False
     # so k and v are brought to q's (autograd casts their gradients back).
     k = k if k.dtype == q.dtype else k.to(q.dtype)
     v = v if v.dtype == q.dtype else v.to(q.dtype)
+    if q.shape[-1] > FLASH_MAX_HEAD_DIM:
+        return _materialised_attention(q, k, v, score_tau, scale, gamma, causal_mask)
     has_gamma = gamma is not None and gamma > 0.0
     o = torch.ops.pnfx.flash_fwd.default(q, k, v, score_tau, float(scale),
                                  float(gamma) if has_gamma else 0.0, has_gamma,
@@ -151,7 +173,9 @@ def flash_pn_fir_tau_attention(
 
     Returns O [B, H, N, d] (contiguous).  scale defaults to 1/sqrt(d).
     Backward is deterministic (no atomics) and returns grads for q, k_tilde, v and
-    score_tau (src/triton_pnfirtau.py:814-983).
+    score_tau (src/triton_pnfirtau.py:814-983).  Any head size: 16, 32, 64 and 128 have
+    kernels, other sizes up to 128 are zero-padded to the next of these, and larger heads
+    take the materialised-score path (_materialised_attention).
     """
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
@@ -172,6 +196,9 @@ def flash_pn_fir_tau_attention_with_stats(q, k_tilde, v, score_tau, scale=None, 
     """
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
+    if q.shape[-1] > FLASH_MAX_HEAD_DIM:
+        raise ValueError(f"head dim {q.shape[-1]}: the flash statistics exist for head sizes up "
+                         f"to {FLASH_MAX_HEAD_DIM} (larger heads run the materialised path)")
     has_gamma = gamma is not None and gamma > 0.0
     k_tilde = k_tilde if k_tilde.dtype == q.dtype else k_tilde.to(q.dtype)
     v = v if v.dtype == q.dtype else v.to(q.dtype)

@@ -69,6 +69,48 @@ def test_flash_matches_oracle(dev, dtype, B, H, N, D, tau, gamma, causal):
     assert_sum_close(float(dtau), rdt, dabs, tol, "dtau")
 
 
+# Head sizes without a kernel of their own: up to 128 zero-padded to the next of 16, 32, 64,
+# 128 inside the ops (the reference pads to next_pow2(max(D, 16)), src/triton_pnfirtau.py:839-841);
+# above 128 the materialised-score path (fp32 scores, the HIP row kernel, fp32 W V).
+ODD_HEAD_CASES = [
+    (1, 2, 100, 8, 0.0, 0.5, True),
+    (2, 1, 77, 24, 0.1, None, True),
+    (1, 2, 130, 48, 0.0, 0.5, False),
+    (1, 1, 200, 80, -0.1, 0.5, True),
+    (1, 2, 65, 96, 0.2, 0.25, True),
+    (1, 2, 150, 256, 0.0, 0.5, True),
+    (1, 1, 90, 256, 0.1, None, False),
+    (1, 1, 64, 192, 0.0, 0.5, True),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,H,N,D,tau,gamma,causal", ODD_HEAD_CASES)
+def test_flash_any_head_dim_matches_oracle(dev, dtype, B, H, N, D, tau, gamma, causal):
+    test_flash_matches_oracle(dev, dtype, B, H, N, D, tau, gamma, causal)
+
+
+def test_flash_module_with_head_dim_256(dev):
+    """PnFirConfig(d_model=1024, n_heads=4): head size 256 runs in PnFirTauFlashMHA (forward and
+    backward) and agrees with the eager PnFirTauMHA (the reference module's composition) at fp32."""
+    from paper_01_anti_decoy_pnfirtau_amd import PnFirConfig, PnFirTauFlashMHA, PnFirTauMHA
+
+    cfg = PnFirConfig(d_model=1024, n_heads=4)
+    torch.manual_seed(3)
+    eager = PnFirTauMHA(cfg).to(dev)
+    flash = PnFirTauFlashMHA(cfg).to(dev)
+    flash.load_state_dict(eager.state_dict())
+    x = torch.randn(2, 96, 1024, device=dev)
+    xs = [x.clone().requires_grad_(True) for _ in range(2)]
+    ys = [m(t) for m, t in zip((eager, flash), xs)]
+    dy = torch.randn_like(ys[0])
+    for y in ys:
+        y.backward(dy)
+    assert_close(to_np64(ys[1]), to_np64(ys[0]), F32_TOL, F32_TOL, "out")
+    assert_close(to_np64(xs[1].grad), to_np64(xs[0].grad), 1e-4, 1e-4, "dx")
+    assert_close(float(flash.score_tau.grad), float(eager.score_tau.grad), 1e-4, 1e-4, "dtau")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("B,H,N,D,tau,gamma,causal", CASES)
 def test_flash_stats_match_oracle(dev, dtype, B, H, N, D, tau, gamma, causal):
