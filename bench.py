@@ -19,7 +19,7 @@ Also measured in the same run and reported on the same JSON line:
   Infinity Cache cannot serve repeats, beside a device copy of the same bytes and the
   FIR's adjoint (the key gradient);
 * ``wide_head``: config C5 (B=8, H=8, N=4096, d=128) TFLOP/s;
-* ``flash_fp32``: the fp32 flash path (B=1, H=8, N=2048, d=64), ms per fwd+bwd step;
+* ``flash_fp32``: the fp32 flash path (B=1, H=8, N=2048, d=64, fp32 MFMA), ms per fwd+bwd step;
 * ``fir_fused_forward``: C4 forward from raw keys, FIR + flash forward against the forward
   with the FIR fused into its key-tile load;
 * ``cpu_baseline``: the reference's CPU path on this host's cores -- the eager
@@ -276,6 +276,22 @@ def bench_fir_sweep(dev):
             "copy_frac_hbm": round(r["same_bytes_copy_gbps"] / PEAK_HBM_GBPS, 4)}
         torch.cuda.empty_cache()
     return out
+
+
+F32 = dict(B=1, H=8, N=2048, D=64)
+
+
+def bench_f32(dev, steps=20, warmup=5):
+    """The fp32 flash path (the reference's TF32-off parity protocol, on the fp32 MFMA): one
+    autograd forward + backward per step at B=1, H=8, N=2048, d=64, tau = 0."""
+    qf, kf, vf, dOf = (t.float() for t in make_inputs(F32["B"], F32["H"], F32["N"], F32["D"], 2, dev))
+    wallf, _ = time_steps(flash_step_fn(qf, kf, vf, dOf, 0.0), steps, warmup)
+    flopsf = 7 * gemm_flops(F32["B"], F32["H"], F32["N"], F32["D"])
+    return {"config": F32, "ms_per_step": round(wallf, 4),
+            "tflops": round(flopsf / (wallf * 1e-3) / 1e12, 3),
+            "frac_fp32_mfma_peak": round(flopsf / (wallf * 1e-3) / 157.3e12, 4),
+            "path": "fp32 kernels (csrc/flash_f32.hip): scores on v_mfma_f64_16x16x4_f64, "
+                    "the other products on v_mfma_f32_16x16x4_f32"}
 
 
 def _graph_ms(fn, reps=20, replays=10):
@@ -699,7 +715,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["flash", "flash_c5", "flash_silent", "fir", "fir_sweep", "fir_fused", "copy", "host",
+    ap.add_argument("--only", choices=["flash", "flash_c5", "flash_silent", "fir", "fir_sweep", "fir_fused", "copy", "host", "f32",
                                        "lm", "mha6", "ref", "kernels", "rows"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -726,6 +742,9 @@ def main():
         return
     if args.only == "lm":
         print(json.dumps(bench_lm(dev)))
+        return
+    if args.only == "f32":
+        print(json.dumps({"flash_fp32": bench_f32(dev)}))
         return
     if args.only == "host":
         print(json.dumps({"host_overhead": bench_host_overhead(dev)}))
@@ -812,12 +831,8 @@ def main():
     flops5 = 7 * gemm_flops(B5, H5, N5, D5)
     del q5, k5, v5, dO5
 
-    # fp32 flash (the parity path: one lane per query row, scalar FMA, no MFMA)
-    F32 = dict(B=1, H=8, N=2048, D=64)
-    qf, kf, vf, dOf = (t.float() for t in make_inputs(F32["B"], F32["H"], F32["N"], F32["D"], 2, dev))
-    wallf, _ = time_steps(flash_step_fn(qf, kf, vf, dOf, 0.0), 5, 2)
-    flopsf = 7 * gemm_flops(F32["B"], F32["H"], F32["N"], F32["D"])
-    del qf, kf, vf, dOf
+    # fp32 flash (the reference's TF32-off parity path, on the fp32 MFMA)
+    f32 = bench_f32(dev)
 
     fir_fused = bench_fir_fused(dev)
     lm = bench_lm(dev)
@@ -862,10 +877,7 @@ def main():
                       "step_event_ms": spread(per5),
                       "tflops": round(flops5 / (wall5 * 1e-3) / 1e12, 2),
                       "kernel_ms": {n: r["ms"] for n, r in kern5.items()}},
-        "flash_fp32": {"config": F32, "ms_per_step": round(wallf, 4),
-                       "tflops": round(flopsf / (wallf * 1e-3) / 1e12, 3),
-                       "path": "fp32 parity kernels (csrc/flash_f32.hip): one lane per query row, "
-                               "scalar FMA, no MFMA"},
+        "flash_fp32": f32,
         "fir_fused_forward": fir_fused,
         "lm_step": lm,
         "mha6_stack": mha6,
