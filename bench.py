@@ -258,6 +258,7 @@ def bench_fir(dev, reps=200, pairs=20, B=8):
             "buffers": f"{pairs} pairs x {nbytes >> 20} MiB",
             "same_bytes_copy_us": round(cus, 3),
             "same_bytes_copy_gbps": round(nbytes / (cus * 1e-6) / 1e9, 1),
+            "frac_of_copy": round(cus / us, 3),
             "adjoint_us_per_launch": round(us_adj, 3),
             "adjoint_gbps": round(nbytes / (us_adj * 1e-6) / 1e9, 1)}
 
