@@ -755,13 +755,14 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
 // folded into the operands), so every scaled score is below 1 (see pow9_unit) and u9s =
 // u^9 2^-9e.  The dQ kernel rounds f du = (10 f x 2^9e) u9s (dW - D) + tie f D gate'/Nmax (f =
 // scale, or 1 when scale = 0 so that the tau partials keep du).  The D <= 64 dK/dV kernel
-// rounds w = (x 2^10e u9s) s_scaled and dS 2^e (its dK product takes Q 2^-e); the D = 128 one
+// rounds w = (x 2^10e u9s) s_scaled and dS 2^e / (10 scale) (its dK product takes Q 2^-e and
+// the sums are multiplied by 10 scale before they are stored); the D = 128 one
 // uses a = rho u (rho = x^(1/10), kappa = 10 scale rho): w = a^10, dS = a^9 (kappa dW -
 // kappa D) + tie.
 // The row constants are eight planes of N floats per (b, h): M, -D, D gate'(M) (the tie
 // gradient of du for a single tie), x, then for D <= 64: M 2^-e, -tau 2^-e, x 2^10e; for
 // D = 128: rho, kappa, -kappa D; plane 7 is the dK/dV kernel's tie term of dS per tied key
-// (for D <= 64 times 2^e), written by the dQ kernel, which counts the ties.
+// (for D <= 64 times 2^e / (10 scale)), written by the dQ kernel, which counts the ties.
 // Exponent e of a row peak, M = m 2^e with m in [0.5, 1) (0 for silent rows), kept within
 // +-64: a peak below 2^-64 then scales to below 1 all the same, and one above 2^64 has already
 // overflowed the forward's u^10.
@@ -1153,9 +1154,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
     c += __shfl_xor(c, 32, 64);
     const int qrow = qrow0 + 16 * qb + r16;
     if (g == 0 && qrow < N) {
-      // dS per tied key (D <= 64: times 2^e, the dK/dV kernel's units)
-      const float ts = scale * rDg[qb];
-      rc_plane(p, bh, 7)[qrow] = c > 0 ? (XT ? __builtin_amdgcn_ldexpf(ts, rE[qb]) : ts) / (float)c : 0.f;
+      // dS per tied key; D <= 64 in the dK/dV kernel's units, dS 2^e / (10 scale)
+      const float ts = XT ? __builtin_amdgcn_ldexpf(rDg[qb], rE[qb]) / 10.f : scale * rDg[qb];
+      rc_plane(p, bh, 7)[qrow] = c > 0 ? ts / (float)c : 0.f;
       double rs = (double)adt[qb][0];
       if (c > 1) rs -= (double)rT0[qb] * (double)(c - 1);
       dsum += rs;
@@ -1280,13 +1281,14 @@ __device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], c
 
 // D <= 64 form: the scores are peak-normalised (scaled by 2^-e per row, see pow9_unit).  With
 // aw = u9s x 2^10e = x u^9 2^e (rc plane 4 holds x 2^10e), the dV weight w = aw s = x u^10 is
-// written over s, and dS 2^e = (aw c) dw + [u == M] T 2^e over dw = dW - D, c = 10 scale:
-// both are the reference's values, to be rounded to bf16 once (dS 2^e rounds as dS does, and
-// the dK product takes Q 2^-e).  rc holds the planes (M 2^-e, -D, T 2^e per tied key,
-// -tau 2^-e, x 2^10e).
+// written over s, and dS 2^e / c = aw dw + [u == M] T 2^e / c over dw = dW - D, c = 10 scale:
+// the reference's w and its dS up to the constant factor c, each to be rounded to bf16 once
+// (dS 2^e / c rounds as dS does, to the same relative precision; the dK product takes Q 2^-e
+// and the kernel multiplies its dK sums by c before they are stored).  rc holds the planes
+// (M 2^-e, -D, T 2^e / c per tied key, -tau 2^-e, x 2^10e).
 template <int KB>
 __device__ __forceinline__ void w_ds_qk_x(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const float* rc,
-                                          int pitch, int r4, float c) {
+                                          int pitch, int r4) {
 #pragma unroll
   for (int qq = 0; qq < 2; ++qq) {
     const f32x4 m4 = *reinterpret_cast<const f32x4*>(rc + r4 + 4 * qq);
@@ -1300,7 +1302,7 @@ __device__ __forceinline__ void w_ds_qk_x(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB],
         const float aw = pow9_unit(sv) * x4[i];
         s[qq][kb][i] = aw * sv;                           // 0 for sv <= 0 (u9s = 0)
         const float tie = (sv == m4[i]) ? t4[i] : 0.f;  // M > 0; T = 0 on silent rows
-        dw[qq][kb][i] = __builtin_fmaf(aw * c, dw[qq][kb][i], tie);
+        dw[qq][kb][i] = __builtin_fmaf(aw, dw[qq][kb][i], tie);
       }
   }
 }
@@ -1308,7 +1310,7 @@ __device__ __forceinline__ void w_ds_qk_x(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB],
 // w_ds_qk_x without the peak-tie term (no row of the half has a key of this wave at its peak).
 template <int KB>
 __device__ __forceinline__ void w_ds_qk_x_notie(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB],
-                                                const float* rc, int pitch, int r4, float c) {
+                                                const float* rc, int pitch, int r4) {
 #pragma unroll
   for (int qq = 0; qq < 2; ++qq) {
     const f32x4 x4 = *reinterpret_cast<const f32x4*>(rc + 4 * pitch + r4 + 4 * qq);
@@ -1319,7 +1321,7 @@ __device__ __forceinline__ void w_ds_qk_x_notie(f32x4 (&s)[2][KB], f32x4 (&dw)[2
         const float sv = s[qq][kb][i];
         const float aw = pow9_unit(sv) * x4[i];
         s[qq][kb][i] = aw * sv;
-        dw[qq][kb][i] = (aw * c) * dw[qq][kb][i];
+        dw[qq][kb][i] = aw * dw[qq][kb][i];
       }
   }
 }
@@ -1410,7 +1412,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   // current tile wait for the prefetch of the next one.  Row constants are five planes of the
   // tile's rows: a lane reads the four consecutive rows its registers cover as one f32x4 per
   // plane (broadcast within a 16-lane group; the four groups' rows are 8 apart, in different
-  // banks).  XT: (M 2^-e, -D, T 2^e per tied key, -tau 2^-e, x 2^10e); D = 128: (M, rho,
+  // banks).  XT: (M 2^-e, -D, T 2^e / c_ds per tied key, -tau 2^-e, x 2^10e); D = 128: (M, rho,
   // kappa, -kappa D, G/Nmax).
   constexpr int NPL = 5;
   __shared__ __attribute__((aligned(16))) bf16 Qs0[BMQ * DK];
@@ -1463,7 +1465,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const bool live = has_keys && wact;
   const float ntau = -p.tau[0];
   const float scale = p.scale;
-  const float c_ds = 10.f * scale;  // XT: dS = (aw c) dw + tie
+  const float c_ds = 10.f * scale;  // XT: the dK sums take dS / c_ds
   const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
 
   bf16x8 kf[KB][KS], vf[KB][KS];
@@ -1592,8 +1594,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         if (masked) mask_qk<KB>(s, m0, hf, kw0, N, CAUSAL, g, r16);
         // rows 32 hf + 8 g + 4 qq + (0..3) of the tile are perm_row(2 hf + qq, 4 g + i)
         if constexpr (XT) {
-          if (ties) w_ds_qk_x<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g, c_ds);
-          else w_ds_qk_x_notie<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g, c_ds);
+          if (ties) w_ds_qk_x<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
+          else w_ds_qk_x_notie<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
         } else {
           if (ties) w_ds_qk<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
           else w_ds_qk_notie<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
@@ -1635,7 +1637,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         bf16x4 k4, v4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          k4[i] = (bf16)adk[db][kb][i];
+          k4[i] = (bf16)(XT ? adk[db][kb][i] * c_ds : adk[db][kb][i]);
           v4[i] = (bf16)adv[db][kb][i];
         }
         *reinterpret_cast<bf16x4*>(dK + (int64_t)key * p.dksn + 16 * db + 4 * g) = k4;
