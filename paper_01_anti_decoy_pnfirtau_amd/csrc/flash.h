@@ -35,7 +35,7 @@ struct BwdParams {
   const uint8_t* mask;
   float* rc;         // row constants [B*H*N][8], layout private to each dtype's kernels
   double* partials;  // tau partials, one per wave of the dq kernel (bf16: [B*H][N/BM][4])
-  void* qs;          // bf16, D <= 64: Q rows scaled by 2^-e (exactly; 2^e the power of two of
+  void* qs;          // bf16: Q rows scaled by 2^-e (exactly; 2^e the power of two of
                      // the row's peak), contiguous [B*H, N, D]: the dK/dV kernel's scores and
                      // its dK product
   uint8_t* ktact;    // [B*H][nk64]: 64-key tiles with any active tile-mask entry (mask given)
@@ -58,8 +58,8 @@ inline int bwd_nkvb(int64_t N, int64_t D) {
   return (int)((N + bnk - 1) / bnk);
 }
 // Workspace of the backward: row constants, tau partials (fp64, one per wave of the bf16 dq
-// kernel, four per workgroup; the fp32 kernels use one per 64 rows), and for D <= 64 the
-// peak-normalised copy of Q that the bf16 dK/dV kernel reads, one activity byte per 64-key
+// kernel, four per workgroup; the fp32 kernels use one per 64 rows), the peak-normalised
+// copy of Q that the bf16 dK/dV kernel reads, one activity byte per 64-key
 // tile, and the activity/tie map of the 32-query x 64-key sub-tiles (written by a dQ wave of
 // 32 rows, so only where the dQ kernel runs two 16-row blocks per wave: D <= 64).
 // The activity/tie map of the backward (BwdParams::amap) is kept up to this sequence length:
@@ -72,7 +72,7 @@ struct BwdWorkspace {
     const int64_t slots = B * H * ((N + rw - 1) / rw) * 4;
     rc_bytes = round256(B * H * N * 8 * 4);
     parts_bytes = round256(slots * 8);
-    xt_bytes = D <= 64 ? round256(B * H * N * D * 2) : 0;  // Q 2^-e
+    xt_bytes = round256(B * H * N * D * 2);  // Q 2^-e
     kt_bytes = round256(B * H * ((N + 63) / 64));
     amap_bytes = (N <= kAmapMaxN && dq_qblocks(D) == 2)
                      ? round256(B * H * ((N + 31) / 32) * ((N + 63) / 64))

@@ -754,15 +754,12 @@ __global__ __launch_bounds__(256, D <= 64 && !FIRK ? 3 : 2) void flash_fwd_kerne
 // M = m 2^e (m in [0.5, 1)) the scores are computed scaled by 2^-e (exactly: a power of two
 // folded into the operands), so every scaled score is below 1 (see pow9_unit) and u9s =
 // u^9 2^-9e.  The dQ kernel rounds f du = (10 f x 2^9e) u9s (dW - D) + tie f D gate'/Nmax (f =
-// scale, or 1 when scale = 0 so that the tau partials keep du).  The D <= 64 dK/dV kernel
-// rounds w = (x 2^10e u9s) s_scaled and dS 2^e / (10 scale) (its dK product takes Q 2^-e and
-// the sums are multiplied by 10 scale before they are stored); the D = 128 one
-// uses a = rho u (rho = x^(1/10), kappa = 10 scale rho): w = a^10, dS = a^9 (kappa dW -
-// kappa D) + tie.
+// scale, or 1 when scale = 0 so that the tau partials keep du).  The dK/dV kernel rounds
+// w = (x 2^10e u9s) s_scaled and dS 2^e / (10 scale) (its dK product takes Q 2^-e and the
+// sums are multiplied by 10 scale before they are stored).
 // The row constants are eight planes of N floats per (b, h): M, -D, D gate'(M) (the tie
-// gradient of du for a single tie), x, then for D <= 64: M 2^-e, -tau 2^-e, x 2^10e; for
-// D = 128: rho, kappa, -kappa D; plane 7 is the dK/dV kernel's tie term of dS per tied key
-// (for D <= 64 times 2^e / (10 scale)), written by the dQ kernel, which counts the ties.
+// gradient of du for a single tie), x, M 2^-e, -tau 2^-e, x 2^10e, and plane 7, the dK/dV
+// kernel's tie term of dS 2^e / (10 scale) per tied key, written by the dQ kernel, which counts the ties.
 // Exponent e of a row peak, M = m 2^e with m in [0.5, 1) (0 for silent rows), kept within
 // +-64: a peak below 2^-64 then scales to below 1 all the same, and one above 2^64 has already
 // overflowed the forward's u^10.
@@ -819,18 +816,11 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(BwdParams p) {
     rc_plane(p, bh, 1)[i] = -Dv;
     rc_plane(p, bh, 2)[i] = Dv * dgate;
     rc_plane(p, bh, 3)[i] = x;
-    if (D <= 64) {  // the peak-normalised form of the dK/dV kernel
-      const int e = peak_exponent(M);
-      rc_plane(p, bh, 4)[i] = __builtin_amdgcn_ldexpf(M, -e);
-      rc_plane(p, bh, 5)[i] = __builtin_amdgcn_ldexpf(-p.tau[0], -e);
-      rc_plane(p, bh, 6)[i] = __builtin_amdgcn_ldexpf(x, 10 * e);
-    } else {  // the a = rho u form of the D = 128 dK/dV kernel
-      const float rho = powf(x, 0.1f);
-      const float kappa = 10.f * p.scale * rho;
-      rc_plane(p, bh, 4)[i] = rho;
-      rc_plane(p, bh, 5)[i] = kappa;
-      rc_plane(p, bh, 6)[i] = -kappa * Dv;
-    }
+    // the peak-normalised form of the dK/dV kernel
+    const int e = peak_exponent(M);
+    rc_plane(p, bh, 4)[i] = __builtin_amdgcn_ldexpf(M, -e);
+    rc_plane(p, bh, 5)[i] = __builtin_amdgcn_ldexpf(-p.tau[0], -e);
+    rc_plane(p, bh, 6)[i] = __builtin_amdgcn_ldexpf(x, 10 * e);
   }
 }
 
@@ -909,7 +899,6 @@ __device__ __forceinline__ bool peak_tie(const f32x4 (&s)[2][QB], const float (&
 // workgroups, two per CU) instead of running one 128-row workgroup per CU.
 template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
-  constexpr bool XT = D <= 64;  // writes the peak-normalised Q of the dK/dV kernel
   // Query rows per wave: 32 (two 16-row MFMA blocks) up to D = 64; 16 at D = 128, where the
   // dQ accumulators and the Q/dO fragments of 32 rows would not fit two workgroups per CU.
   constexpr int QB = dq_qblocks(D), RPW = 16 * QB;
@@ -956,8 +945,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
   f32x4 dw_init[QB];  // -D: the dW accumulator starts there
   f32x4 s_init[QB];   // the score accumulator starts at -tau 2^-e (scale folded into Q)
   float sc_e[QB], nt_e[QB];  // scale 2^-e and -tau 2^-e, for scales that are not folded
-  // D <= 64, for the dK/dV kernel (which runs next): the rows of Q scaled by 2^-e.
-  bf16* Qs = XT ? static_cast<bf16*>(p.qs) + (int64_t)bh * N * D : nullptr;
+  // For the dK/dV kernel (which runs next): the rows of Q scaled by 2^-e.
+  bf16* Qs = static_cast<bf16*>(p.qs) + (int64_t)bh * N * D;
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int row = qrow0 + 16 * qb + r16;
@@ -981,7 +970,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
       const bool ok = rok && col < D;
       qf[qb][ks] = ok ? ld16(Q + (int64_t)row * p.qsn + col) : zero_bf16x8();
       dof[qb][ks] = ok ? ld16(dO + (int64_t)row * p.dosn + col) : zero_bf16x8();
-      if (XT && ok)
+      if (ok)
         *reinterpret_cast<bf16x8*>(Qs + (int64_t)row * D + col) =
             scale_frag(qf[qb][ks], __builtin_amdgcn_ldexpf(1.f, -rE[qb]));
       if (PS) qf[qb][ks] = scale_frag(qf[qb][ks], sc_e[qb]);  // a power of two: exact
@@ -1154,8 +1143,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
     c += __shfl_xor(c, 32, 64);
     const int qrow = qrow0 + 16 * qb + r16;
     if (g == 0 && qrow < N) {
-      // dS per tied key; D <= 64 in the dK/dV kernel's units, dS 2^e / (10 scale)
-      const float ts = XT ? __builtin_amdgcn_ldexpf(rDg[qb], rE[qb]) / 10.f : scale * rDg[qb];
+      // dS per tied key in the dK/dV kernel's units, dS 2^e / (10 scale)
+      const float ts = __builtin_amdgcn_ldexpf(rDg[qb], rE[qb]) / 10.f;
       rc_plane(p, bh, 7)[qrow] = c > 0 ? ts / (float)c : 0.f;
       double rs = (double)adt[qb][0];
       if (c > 1) rs -= (double)rT0[qb] * (double)(c - 1);
@@ -1194,10 +1183,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_kernel(BwdParams p) {
 }
 
 // dK and dV: key-parallel.  Each wave owns KPW consecutive keys (32 for D <= 64, 16 for
-// D = 128) held as MFMA B fragments; the workgroup streams 64-row query tiles (Q and dO, for
-// D <= 64 also their row-scaled copies, plus the row constants) through LDS from the last
-// query tile back to the causal diagonal; the transposed operands come from the same tiles
-// through transposing reads.
+// D = 128) held as MFMA B fragments; the workgroup streams 64-row query tiles (Q 2^-e and
+// dO, plus the row constants) through LDS from the last query tile back to the causal
+// diagonal; the transposed operands come from the same tiles through transposing reads.
 template <int D>
 struct DkdvCfg {
   static constexpr int KPW = D <= 64 ? 32 : 16;
@@ -1205,24 +1193,11 @@ struct DkdvCfg {
   static constexpr int BNK = 4 * KPW;
 };
 
-// In the S layout (key per lane, four query rows per 16-row block), for one 32-row half
-// (query blocks 2*hf, 2*hf+1): w = u^10 g/Z written over s and ds written over dw.
 // Query-major layout S (register i of lane group g holds query perm_row(blk, 4g+i) of the
 // tile, lane r16 holds key 16kb+r16 of the wave's keys): the affine map and the mask, as
 // affine_kq and mask_kq above.
-template <int KB, bool PS>
-__device__ __forceinline__ void affine_qk(f32x4 (&s)[2][KB], float scale, float ntau) {
-  if (PS) return;
-#pragma unroll
-  for (int qq = 0; qq < 2; ++qq)
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s[qq][kb][i] = __builtin_fmaf(s[qq][kb][i], scale, ntau);
-}
-
-// affine_qk with a -tau per query row (register i of block qq): the peak-normalised scores of
-// the D <= 64 form, formed from Q 2^-e.
+// The affine map with a -tau per query row (register i of block qq): the peak-normalised
+// scores, formed from Q 2^-e.
 template <int KB, bool PS>
 __device__ __forceinline__ void affine_qk_rows(f32x4 (&s)[2][KB], float scale,
                                                const f32x4 (&ntau)[2]) {
@@ -1251,35 +1226,7 @@ __device__ __forceinline__ void mask_qk(f32x4 (&s)[2][KB], int m0, int hf, int k
     }
 }
 
-// The dV weight w = a^10 over s and dS = a^9 (kappa dW - kappa D) + [u == M] G/Nmax over dw,
-// a = rho u.  rc holds the planes (M, rho, kappa, -kappa D, G/Nmax) of the tile's rows, each
-// `pitch` floats; rows r4 + 4 qq + (0..3) are the four query rows a lane's registers cover in
-// the 16-row block qq.
-template <int KB>
-__device__ __forceinline__ void w_ds_qk(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB], const float* rc,
-                                        int pitch, int r4) {
-#pragma unroll
-  for (int qq = 0; qq < 2; ++qq) {
-    f32x4 c[5];
-#pragma unroll
-    for (int k = 0; k < 5; ++k) c[k] = *reinterpret_cast<const f32x4*>(rc + k * pitch + r4 + 4 * qq);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const float u = relu_mfma(s[qq][kb][i]);
-        const float a = u * c[1][i];
-        const float a2 = a * a;
-        const float a4 = a2 * a2;
-        const float a9 = a4 * a4 * a;
-        s[qq][kb][i] = a9 * a;
-        const float tie = (u == c[0][i]) ? c[4][i] : 0.f;  // G = 0 on silent rows
-        dw[qq][kb][i] = __builtin_fmaf(a9, __builtin_fmaf(c[2][i], dw[qq][kb][i], c[3][i]), tie);
-      }
-  }
-}
-
-// D <= 64 form: the scores are peak-normalised (scaled by 2^-e per row, see pow9_unit).  With
+// The scores are peak-normalised (scaled by 2^-e per row, see pow9_unit).  With
 // aw = u9s x 2^10e = x u^9 2^e (rc plane 4 holds x 2^10e), the dV weight w = aw s = x u^10 is
 // written over s, and dS 2^e / c = aw dw + [u == M] T 2^e / c over dw = dW - D, c = 10 scale:
 // the reference's w and its dS up to the constant factor c, each to be rounded to bf16 once
@@ -1322,29 +1269,6 @@ __device__ __forceinline__ void w_ds_qk_x_notie(f32x4 (&s)[2][KB], f32x4 (&dw)[2
         const float aw = pow9_unit(sv) * x4[i];
         s[qq][kb][i] = aw * sv;
         dw[qq][kb][i] = aw * dw[qq][kb][i];
-      }
-  }
-}
-
-// w_ds_qk without the peak-tie term.
-template <int KB>
-__device__ __forceinline__ void w_ds_qk_notie(f32x4 (&s)[2][KB], f32x4 (&dw)[2][KB],
-                                              const float* rc, int pitch, int r4) {
-#pragma unroll
-  for (int qq = 0; qq < 2; ++qq) {
-    f32x4 c[3];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) c[k] = *reinterpret_cast<const f32x4*>(rc + (k + 1) * pitch + r4 + 4 * qq);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const float a = relu_mfma(s[qq][kb][i]) * c[0][i];
-        const float a2 = a * a;
-        const float a4 = a2 * a2;
-        const float a9 = a4 * a4 * a;
-        s[qq][kb][i] = a9 * a;
-        dw[qq][kb][i] = a9 * __builtin_fmaf(c[1][i], dw[qq][kb][i], c[2][i]);
       }
   }
 }
@@ -1398,10 +1322,8 @@ __device__ __forceinline__ void dtau_sum(const double* partials, int64_t n, floa
 
 template <int D, bool CAUSAL, bool PS>
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
-  // D <= 64: the scores are peak-normalised per row (from the dQ kernel's copy Q 2^-e, which
-  // also serves the dK product) and the weights formed from u9s; D = 128 uses a = rho u on the
-  // raw Q tile.  Either way the tiles are Q (scaled or not) and dO.
-  constexpr bool XT = D <= 64;
+  // The scores are peak-normalised per row (from the dQ kernel's copy Q 2^-e, which also
+  // serves the dK product) and the weights formed from u9s; the tiles are Q 2^-e and dO.
   constexpr int KPW = DkdvCfg<D>::KPW, KB = DkdvCfg<D>::KB, BNK = DkdvCfg<D>::BNK;
   constexpr int BMQ = 64;
   constexpr int DK = D < 32 ? 32 : D;
@@ -1412,8 +1334,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   // current tile wait for the prefetch of the next one.  Row constants are five planes of the
   // tile's rows: a lane reads the four consecutive rows its registers cover as one f32x4 per
   // plane (broadcast within a 16-lane group; the four groups' rows are 8 apart, in different
-  // banks).  XT: (M 2^-e, -D, T 2^e / c_ds per tied key, -tau 2^-e, x 2^10e); D = 128: (M, rho,
-  // kappa, -kappa D, G/Nmax).
+  // banks): M 2^-e, -D, T 2^e / c_ds per tied key, -tau 2^-e, x 2^10e.
   constexpr int NPL = 5;
   __shared__ __attribute__((aligned(16))) bf16 Qs0[BMQ * DK];
   __shared__ __attribute__((aligned(16))) bf16 dOs0[BMQ * DK];
@@ -1429,17 +1350,15 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   int bh, kvb;
   map_block(p.nkvb, p.B * p.H, false, bh, kvb);
   const int b = bh / p.H, h = bh % p.H;
-  const bf16* Q = static_cast<const bf16*>(p.q) + b * p.qsb + h * p.qsh;
   const bf16* K = static_cast<const bf16*>(p.k) + b * p.ksb + h * p.ksh;
   const bf16* V = static_cast<const bf16*>(p.v) + b * p.vsb + h * p.vsh;
   const bf16* dO = static_cast<const bf16*>(p.dout) + b * p.dosb + h * p.dosh;
   // Staging of the row constants: wave w copies one plane of the tile's rows, wave 0 also the
-  // fifth (XT: workspace planes 4, 1, 7, 5, 6; D = 128: 0, 4, 5, 6, 7).
-  const float* RCgw = rc_plane(p, bh, XT ? (w == 0 ? 4 : w == 2 ? 7 : w == 3 ? 5 : 1)
-                                         : (w == 0 ? 0 : 3 + w));
-  const float* RCg4 = rc_plane(p, bh, XT ? 6 : 7);
-  // XT: Q 2^-e, written by the dQ kernel
-  const bf16* Qsc = XT ? static_cast<const bf16*>(p.qs) + (int64_t)bh * N * D : nullptr;
+  // fifth (workspace planes 4, 1, 7, 5, 6).
+  const float* RCgw = rc_plane(p, bh, w == 0 ? 4 : w == 2 ? 7 : w == 3 ? 5 : 1);
+  const float* RCg4 = rc_plane(p, bh, 6);
+  // Q 2^-e, written by the dQ kernel
+  const bf16* Qsc = static_cast<const bf16*>(p.qs) + (int64_t)bh * N * D;
   // The workgroup's 64-key tiles.  With the tile activity of the dQ stage, workgroup j of a
   // (b, h) takes positions TPW j .. TPW j + TPW - 1 of the order "active tiles ascending, then
   // silent tiles": active tiles share workgroups, so no wave idles beside an active one, and
@@ -1463,9 +1382,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   const int kw0 = wtile < 0 ? N : wtile * 64 + (KPW * w) % 64;
   const bool has_keys = kw0 < N;  // the wave writes dK, dV rows (zeros if silent)
   const bool live = has_keys && wact;
-  const float ntau = -p.tau[0];
   const float scale = p.scale;
-  const float c_ds = 10.f * scale;  // XT: the dK sums take dS / c_ds
+  const float c_ds = 10.f * scale;  // the dK sums take dS / c_ds
   const FragLane flr = rt_lane<DK>(r16, g), flt = tr_lane<DK>(lane);
 
   bf16x8 kf[KB][KS], vf[KB][KS];
@@ -1481,7 +1399,6 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
       if (PS) kf[kb][ks] = scale_frag(kf[kb][ks], scale);
     }
   }
-  const f32x4 s_init = PS ? f32x4{ntau, ntau, ntau, ntau} : f32x4{0.f, 0.f, 0.f, 0.f};
   f32x4 adk[DB][KB], adv[DB][KB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -1511,13 +1428,13 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
   // scores are masked), including their row constants.  D <= 64: whole tiles take a scalar
   // base plus the lanes' fixed 32-bit offsets; D = 128, at the register limit, forms every
   // address from the row and column.
-  const TileDma<D, DK> tq(w, lane, XT ? D : p.qsn), tdo(w, lane, p.dosn);
+  const TileDma<D, DK> tq(w, lane, D), tdo(w, lane, p.dosn);
   auto load_tile = [&](int m, const QBuf& bb) {
-    if (XT) {
+    if (D <= 64) {
       tq.load(Qsc, D, m, N, bb.q, w);
       tdo.load(dO, p.dosn, m, N, bb.o, w);
     } else {
-      tq.load_clamped(Q, p.qsn, m, N, bb.q, w);
+      tq.load_clamped(Qsc, D, m, N, bb.q, w);
       tq.load_clamped(dO, p.dosn, m, N, bb.o, w);
     }
     const int row = min(m + lane, N - 1);
@@ -1549,7 +1466,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
     if (work) {
       const bf16* Qc = bc.q;
       const bf16* dOc = bc.o;
-      const bf16* Qt = Qc;    // operand of dK += dS^T Q (XT: dS 2^e and Q 2^-e)
+      const bf16* Qt = Qc;    // operand of dK += dS^T Q (dS 2^e / c_ds and Q 2^-e)
       const bf16* dOt = dOc;  // operand of dV += w^T dO
       const bool masked = (CAUSAL && m0 < kw0 + KPW - 1) || m0 + BMQ > N || kw0 + KPW > N;
 #pragma unroll
@@ -1560,16 +1477,15 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         if (!(code & 1)) continue;          // a silent 32-row half
         const bool ties = (code & tie_bit) != 0;
         f32x4 s[2][KB], dw[2][KB];
-        f32x4 ntr[2];  // XT: -tau 2^-e of the lane's rows in each 16-row block
+        f32x4 ntr[2];  // -tau 2^-e of the lane's rows in each 16-row block
 #pragma unroll
         for (int qq = 0; qq < 2; ++qq) {
-          // XT: the dW accumulator starts at -D of the four rows the lane's registers cover,
-          // the score accumulator at their -tau 2^-e (scale folded into K) or 0 (affine below)
+          // The dW accumulator starts at -D of the four rows the lane's registers cover, the
+          // score accumulator at their -tau 2^-e (scale folded into K) or 0 (affine below)
           const int r4 = 32 * hf + 8 * g + 4 * qq;
-          const f32x4 dw0 = XT ? *reinterpret_cast<const f32x4*>(bc.rc + BMQ + r4)
-                               : f32x4{0.f, 0.f, 0.f, 0.f};
-          if (XT) ntr[qq] = *reinterpret_cast<const f32x4*>(bc.rc + 3 * BMQ + r4);
-          const f32x4 sa0 = (XT && PS) ? ntr[qq] : s_init;
+          const f32x4 dw0 = *reinterpret_cast<const f32x4*>(bc.rc + BMQ + r4);
+          ntr[qq] = *reinterpret_cast<const f32x4*>(bc.rc + 3 * BMQ + r4);
+          const f32x4 sa0 = PS ? ntr[qq] : f32x4{0.f, 0.f, 0.f, 0.f};
           bf16x8 qa[KS], da[KS];
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
@@ -1589,17 +1505,11 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
             dw[qq][kb] = c4;
           }
         }
-        if (XT) affine_qk_rows<KB, PS>(s, scale, ntr);
-        else affine_qk<KB, PS>(s, scale, ntau);
+        affine_qk_rows<KB, PS>(s, scale, ntr);
         if (masked) mask_qk<KB>(s, m0, hf, kw0, N, CAUSAL, g, r16);
         // rows 32 hf + 8 g + 4 qq + (0..3) of the tile are perm_row(2 hf + qq, 4 g + i)
-        if constexpr (XT) {
-          if (ties) w_ds_qk_x<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
-          else w_ds_qk_x_notie<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
-        } else {
-          if (ties) w_ds_qk<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
-          else w_ds_qk_notie<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
-        }
+        if (ties) w_ds_qk_x<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
+        else w_ds_qk_x_notie<KB>(s, dw, bc.rc, BMQ, 32 * hf + 8 * g);
         bf16x8 wf[KB], sf[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
@@ -1637,7 +1547,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(BwdParams p) {
         bf16x4 k4, v4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          k4[i] = (bf16)(XT ? adk[db][kb][i] * c_ds : adk[db][kb][i]);
+          k4[i] = (bf16)(adk[db][kb][i] * c_ds);
           v4[i] = (bf16)adv[db][kb][i];
         }
         *reinterpret_cast<bf16x4*>(dK + (int64_t)key * p.dksn + 16 * db + 4 * g) = k4;
