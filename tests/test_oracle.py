@@ -273,6 +273,36 @@ def test_flash_reference_bf16_rounding_points_known_answers():
         assert np.abs(a - b).max() <= 0.05 * np.abs(b).max() and np.any(a != b)
 
 
+def test_flash_reference_bf16_rounding_points_two_keys():
+    """Two queries, two keys (d = 1, q = (0, 1), k = (1, 1/2), v = (3, 5), dO = 1, scale 1,
+    tau 0, gamma 0.5, causal).  Row 0 is silent (s = 0).  Row 1: u = (1, 1/2),
+    P = (1, 2^-10), Z = 1025/1024, M = 1, g = 2/3, one tie (key 0).
+    * O = (3 + 5 / 1024) g / Z = 6154/3075 = 2.0013..., stored in bf16 as 2.0.
+    * w = P g / Z = (2048/3075, 2/3075), rounded to bf16 for dV: 0.66796875 and
+      0.000652313232421875 (= 171/256 and 171/262144).
+    * D = <dO, O>/g with the stored O: 3 = dW_0, so du_0 is the tie term alone,
+      3 * 0.5 / 1.5^2 = 2/3, and du_1 = (10 g / Z) 2^-9 (5 - 3) = 0.0260162...; dS = du rounded
+      to bf16: 0.66796875 and 0.0260009765625 (= 213/8192).
+    * dq_1 = dS_0 k_0 + dS_1 k_1 = 0.68096923828125, dk = dS (q_1 = 1), dv = bf16(w), and
+      dtau = -(du_0 + du_1) is not rounded.
+    Each value is written out by hand from the reference's rounding points
+    (src/triton_pnfirtau.py:417-420 O and its bf16 store, :566-571 w, :598-600 dS)."""
+    q = np.array([0.0, 1.0]).reshape(1, 1, 2, 1)
+    k = np.array([1.0, 0.5]).reshape(1, 1, 2, 1)
+    v = np.array([3.0, 5.0]).reshape(1, 1, 2, 1)
+    dO = np.ones((1, 1, 2, 1))
+    O_, dq, dk, dv, dt = O.flash_reference_bf16(q, k, v, 0.0, dO, 1.0, 0.5, True)
+    assert O_[0, 0, 0, 0] == 0.0 and O_[0, 0, 1, 0] == 2.0
+    assert dq[0, 0, 0, 0] == 0.0 and dq[0, 0, 1, 0] == 0.68096923828125
+    assert dk[0, 0, 0, 0] == 171 / 256 and dk[0, 0, 1, 0] == 213 / 8192
+    assert dv[0, 0, 0, 0] == 171 / 256 and dv[0, 0, 1, 0] == 171 / 262144
+    du1 = (10 * (2 / 3) / (1025 / 1024 + 1e-12)) * 2.0**-9 * 2.0
+    assert dt == pytest.approx(-(2 / 3 + du1), rel=1e-12)
+    # the exact gradients differ from every rounded one above
+    eq, ek, ev, _ = O.flash_bwd(q, k, v, 0.0, dO, 1.0, 0.5, True)
+    assert ek[0, 0, 1, 0] != dk[0, 0, 1, 0] and ev[0, 0, 0, 0] != dv[0, 0, 0, 0]
+
+
 def test_tile_activity_closed_form_all_active():
     # every causal tile active: fully-silent fraction of the nb^2 grid is (nb-1)/(2nb)
     # (0.46875 at nb = 16, the exp4b convention, results/exp4b_mha6_instrumentation.json:24-157)
