@@ -159,6 +159,27 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert rc == -1 and b"bf16 only" in lib.pnfx_last_error()
 
 
+@pytest.mark.parametrize("B,H,N,D", [(4, 16, 8192, 64), (8, 8, 4096, 128), (1, 3, 520, 128),
+                                     (2, 4, 1000, 32), (1, 1, 70000, 16)])
+def test_backward_workspace_holds_only_what_the_kernels_use(B, H, N, D):
+    """The backward workspace is the sum of its parts, each rounded up to 256 bytes: eight fp32
+    row-constant planes, one fp64 tau partial per dQ wave (32 rows per wave for d <= 64, 16 at
+    d = 128, four waves per workgroup), the bf16 copy Q 2^-e, one activity byte per 64-key tile,
+    and the activity/tie map (a byte per 32-row group and 64-key tile) only where the dQ kernel
+    writes it: d <= 64 and N <= 65536.  At d = 128 (16 rows per dQ wave) no map bytes are held,
+    which keeps C5 well inside the no-allocation entry point's scratch."""
+    r = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    rows_per_wg = 128 if D <= 64 else 64
+    want = (r(B * H * N * 8 * 4) + r(B * H * -(-N // rows_per_wg) * 4 * 8) + r(B * H * N * D * 2)
+            + r(B * H * -(-N // 64)))
+    if D <= 64 and N <= 65536:
+        want += r(B * H * -(-N // 32) * -(-N // 64))
+    lib = _lib.lib()
+    assert lib.pnfx_flash_bwd_workspace_size(B, H, N, D) == want
+    if (B, H, N, D) == (8, 8, 4096, 128):
+        assert want < _lib.PNFX_NOALLOC_SCRATCH_BYTES
+
+
 def test_hip_ops_refuse_cpu_tensors():
     from paper_01_anti_decoy_pnfirtau_amd import ops  # noqa: F401
 
