@@ -721,6 +721,23 @@ def test_flash_previously_failing_draws_match_oracle(dev, case):
     _check_random_case(dev, case)
 
 
+@pytest.mark.xfail(reason="one dQ element at 1.64 against a bar of 1.48: bf16 rounding of dS "
+                          "in a row whose two dS k terms cancel to 0.7 %; reproduced bit for bit "
+                          "by a CPU emulation of the kernels' rounding points", strict=False)
+def test_flash_known_excursion_two_key_cancellation(dev):
+    """The one draw of a 1920-draw sweep (16 seeds beyond the suite's) that goes past the
+    bar: row 2 of (b, h) = (0, 1) has two active keys whose
+    dS_j k_j terms (8.93 * 0.83 and -10.92 * 0.67) cancel to dQ = 0.0623.  The forward
+    weights V by bf16-rounded P, so D = <dO, O>/g moves by 6e-4 relative, which moves dS_0
+    from 8.934 to 8.906, just past the midpoint between the bf16 neighbours 8.875 and 8.9375;
+    dQ comes out 0.00098 (one element of 36608, ratio 1.64 against the bar of 1.25 x the
+    reference rounding's 1.19 on this tensor).  The reference's own rounding points give
+    0.0527 here; neither is a kernel fault, the element is a bf16 rounding of dS that both
+    designs make."""
+    _check_random_case(dev, (2, 2, 143, 64, -0.297, None, True, 0.125, 0.5, True,
+                             torch.bfloat16))
+
+
 def _check_random_case(dev, case):
     B, H, N, D, tau, gamma, causal, scale, std, packed, dtype = case
     print(f"[flash random B={B} H={H} N={N} D={D} tau={tau} gamma={gamma} causal={causal} "
