@@ -162,14 +162,16 @@ void check_qkv(const Tensor& q, const Tensor& k, const Tensor& v) {
   }
 }
 
-// O and its bf16 rounding residual (bf16 only) as two slices of one allocation, each [B,H,N,D];
-// with o_bnhd backed by [B,N,H,D] rows, so that the caller's transpose back to [B,N,H*D] is free.
+// O and its bf16 rounding residual (bf16 only), each [B,H,N,D] and each its own allocation
+// (the schema declares no aliasing between outputs); with o_bnhd backed by [B,N,H,D] rows, so
+// that the caller's transpose back to [B,N,H*D] is free.
 std::pair<Tensor, Tensor> new_o_pair(const Tensor& q, bool o_bnhd, bool with_lo) {
   const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
-  const int64_t n = with_lo ? 2 : 1;
-  Tensor buf = o_bnhd ? at::empty({n, B, N, H, D}, q.options()).permute({0, 1, 3, 2, 4})
-                      : at::empty({n, B, H, N, D}, q.options());
-  return {buf[0], with_lo ? buf[1] : q.new_empty({0})};
+  const auto one = [&]() {
+    return o_bnhd ? at::empty({B, N, H, D}, q.options()).permute({0, 2, 1, 3})
+                  : at::empty({B, H, N, D}, q.options());
+  };
+  return {one(), with_lo ? one() : q.new_empty({0})};
 }
 
 const void* ptr_or_null(const Tensor& t) { return t.numel() ? t.data_ptr() : nullptr; }
@@ -193,8 +195,6 @@ void check_head_dim(int64_t D) {
 // silent-tile bound costs to launch: below it the forward runs without the bound (same results).
 constexpr int64_t kBoundMinScores = int64_t(1) << 26;  // B*H*N^2, e.g. B*H = 64 at N = 1024
 
-int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
-
 std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> flash_fwd_cuda(
     const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, const Tensor& tau, double scale,
     double gamma, bool has_gamma, bool causal, bool o_bnhd, bool with_nmax) {
@@ -217,31 +217,29 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> flash_fwd_cuda(
   const Tensor q = bhnd(q_in, "q", bf), k = bhnd(k_in, "k", bf), v = bhnd(v_in, "v", bf);
   const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
   auto [o, o_lo] = new_o_pair(q, o_bnhd, bf);
-  // M, Z (fp32 [B,H,N]), Nmax (int32, only when asked for), the tile mask (N^2/2048 bytes per
-  // (b, h)) and the silent-tile bound's workspace: slices of one allocation, 256-byte aligned
+  // M, Z (fp32 [B,H,N]), Nmax (int32, only when asked for) and the tile mask (N^2/2048 bytes
+  // per (b, h)), each its own allocation, and the silent-tile bound's workspace
   const int64_t rows = B * H * N;
   const auto ms = mask_shape(B, H, N);
   const int64_t mn = ms[0] * ms[1] * ms[2];
   const int64_t nws = (rows && B * H * N * N >= kBoundMinScores)
                           ? pnfx_flash_fwd_workspace_size(B, H, N, D) : 0;
-  const int64_t sb = round256(4 * rows), nmb = with_nmax ? sb : 0, mb = round256(mn);
-  Tensor buf = at::empty({2 * sb + nmb + mb + nws}, q.options().dtype(at::kByte));
-  Tensor M = buf.narrow(0, 0, 4 * rows).view(at::kFloat).view({B, H, N});
-  Tensor Z = buf.narrow(0, sb, 4 * rows).view(at::kFloat).view({B, H, N});
-  Tensor Nm = with_nmax ? buf.narrow(0, 2 * sb, 4 * rows).view(at::kInt).view({B, H, N})
-                        : buf.narrow(0, 0, 0).view(at::kInt);
-  Tensor mask = buf.narrow(0, 2 * sb + nmb, mn).view({ms[0], ms[1], ms[2]});
+  const auto f32 = q.options().dtype(at::kFloat);
+  Tensor M = at::empty({B, H, N}, f32), Z = at::empty({B, H, N}, f32);
+  Tensor Nm = at::empty(with_nmax ? at::IntArrayRef{B, H, N} : at::IntArrayRef{0},
+                        q.options().dtype(at::kInt));
+  Tensor mask = at::empty({ms[0], ms[1], ms[2]}, q.options().dtype(at::kByte));
   if (rows == 0) return {o, o_lo, M, Z, Nm, mask};  // empty input: empty outputs
+  Tensor ws = at::empty({nws}, q.options().dtype(at::kByte));
   const c10::DeviceGuard guard(q.device());
   const Tensor t32 = tau32(tau);
-  uint8_t* base = buf.data_ptr<uint8_t>();
   check_rc(pnfx_flash_fwd(q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(),
                           k.stride(0), k.stride(1), k.stride(2), v.data_ptr(), v.stride(0),
                           v.stride(1), v.stride(2), o.data_ptr(), o.stride(0), o.stride(1),
                           o.stride(2), bf ? o_lo.data_ptr() : nullptr, M.data_ptr<float>(),
                           Z.data_ptr<float>(), with_nmax ? Nm.data_ptr<int32_t>() : nullptr,
-                          mn ? base + 2 * sb + nmb : nullptr,
-                          nws ? base + 2 * sb + nmb + mb : nullptr, nws, B, H, N, D,
+                          mn ? mask.data_ptr<uint8_t>() : nullptr,
+                          nws ? ws.data_ptr() : nullptr, nws, B, H, N, D,
                           t32.data_ptr<float>(), (float)scale, (float)gamma, has_gamma, causal,
                           code, stream_of(q)),
            "pnfx_flash_fwd");
@@ -277,14 +275,10 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> flash_bwd_cuda(
   const Tensor dout = bhnd(do_in.scalar_type() == q.scalar_type() ? do_in : do_in.to(q.scalar_type()),
                            "dO", bf);
   const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
-  // dQ, dK, dV and dtau: slices of one allocation
-  const int64_t gb = B * H * N * D * q.element_size();
-  Tensor grads = at::empty({3 * gb + 256}, q.options().dtype(at::kByte));
-  const auto grad = [&](int i) {
-    return grads.narrow(0, i * gb, gb).view(q.scalar_type()).view({B, H, N, D});
-  };
-  Tensor dq = grad(0), dk = grad(1), dv = grad(2);
-  Tensor dtau = grads.narrow(0, 3 * gb, 4).view(at::kFloat);
+  // dQ, dK, dV and dtau, each its own allocation (returned to autograd as the inputs' grads)
+  Tensor dq = at::empty({B, H, N, D}, q.options()), dk = at::empty({B, H, N, D}, q.options());
+  Tensor dv = at::empty({B, H, N, D}, q.options());
+  Tensor dtau = at::empty({1}, q.options().dtype(at::kFloat));
   if (B * H * N == 0) return {dq, dk, dv, dtau.zero_()};  // -(sum over no scores) = 0
   const c10::DeviceGuard guard(q.device());
   const int64_t wsb = pnfx_flash_bwd_workspace_size(B, H, N, D);
@@ -315,8 +309,8 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> flash_fwd_fir_cuda(
   const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
   const Tensor taps2 = taps.reshape({-1, taps.size(-1)}).to(q.device(), at::kFloat).contiguous();
   auto [o, o_lo] = new_o_pair(q, o_bnhd, true);
-  Tensor stats = at::empty({2, B, H, N}, q.options().dtype(at::kFloat));
-  Tensor M = stats[0], Z = stats[1];
+  const auto f32 = q.options().dtype(at::kFloat);
+  Tensor M = at::empty({B, H, N}, f32), Z = at::empty({B, H, N}, f32);
   const auto ms = mask_shape(B, H, N);
   Tensor mask = at::empty({ms[0], ms[1], ms[2]}, q.options().dtype(at::kByte));
   if (B * H * N == 0) return {o, o_lo, M, Z, mask};

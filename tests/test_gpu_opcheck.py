@@ -1,0 +1,52 @@
+"""torch.library.opcheck over the C++-registered pnfx operators: the schema's mutation and
+aliasing claims, the autograd registration, the fake (meta) kernels against the real
+kernels' outputs, and tracing through AOTAutograd with dynamic shapes -- what torch.compile
+relies on.  Small shapes; bf16 and fp32."""
+import pytest
+import torch
+
+from paper_01_anti_decoy_pnfirtau_amd import ops  # noqa: F401  (loads the ops and fakes)
+from tests.helpers import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_opcheck_flash_forward_and_backward(dev, dtype):
+    B, H, N, D = 1, 2, 80, 64
+    q, k, v, dO = (seeded((B, H, N, D), 300 + i, dtype, dev) for i in range(4))
+    tau = torch.tensor(0.05, device=dev)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    torch.library.opcheck(torch.ops.pnfx.flash_fwd.default,
+                          (qg, kg, vg, tau, 0.125, 0.5, True, True, False, False))
+    torch.library.opcheck(torch.ops.pnfx.flash_fwd.default,
+                          (q, k, v, tau, 0.125, 0.5, True, True, True, True))
+    o, o_lo, M, Z, _, mask = torch.ops.pnfx.flash_fwd(q, k, v, tau, 0.125, 0.5, True, True,
+                                                      False, False)
+    torch.library.opcheck(torch.ops.pnfx.flash_bwd.default,
+                          (q, k, v, tau, o, o_lo, dO, M, Z, mask, 0.125, 0.5, True, True))
+
+
+def test_opcheck_fused_fir_forward(dev):
+    B, H, N, D = 2, 2, 90, 32
+    q, kr, v = (seeded((B, H, N, D), 310 + i, torch.bfloat16, dev) for i in range(3))
+    taps = torch.rand(7, device=dev)
+    tau = torch.tensor(0.0, device=dev)
+    torch.library.opcheck(torch.ops.pnfx.flash_fwd_fir.default,
+                          (q, kr, v, tau, taps, D ** -0.5, 0.5, True, True, False))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_opcheck_fir_and_row_scores(dev, dtype):
+    x = seeded((2, 70, 48), 320, dtype, dev).requires_grad_(True)
+    taps = torch.rand(7, device=dev)
+    torch.library.opcheck(torch.ops.pnfx.fir_fwd.default, (x, taps))
+    torch.library.opcheck(torch.ops.pnfx.fir_bwd.default, (x.detach(), taps))
+    raw = seeded((1, 2, 40, 40), 321, dtype, dev).requires_grad_(True)
+    tau = torch.tensor(0.1, device=dev)
+    torch.library.opcheck(torch.ops.pnfx.pn_rows_fwd.default,
+                          (raw, tau, 0.125, 10.0, 0.5, True, True))
+    w, M, Z, Nm = torch.ops.pnfx.pn_rows_fwd(raw.detach(), tau, 0.125, 10.0, 0.5, True, True)
+    torch.library.opcheck(torch.ops.pnfx.pn_rows_bwd.default,
+                          (torch.randn_like(w), raw.detach(), tau, M, Z, Nm, 0.125, 10.0, 0.5,
+                           True, True))

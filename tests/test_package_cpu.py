@@ -237,6 +237,46 @@ def test_flash_op_checks_operand_agreement_on_the_host():
         ops._check_qkv(q, q.to("meta"), q)
 
 
+def test_fake_kernels_give_the_output_layouts():
+    """Under FakeTensorMode (what torch.compile traces with) every pnfx op returns tensors of
+    the real kernels' shapes, dtypes and memory order without touching a device: O as
+    [B, H, N, D] or, with o_bnhd, as a [B, H, N, D] view of [B, N, H, D] rows; M and Z fp32
+    [B, H, N]; Nmax int32 only when asked for; the tile mask [B*H, ceil(N/32), ceil(N/64)];
+    the backward's gradients contiguous and dtau one fp32; the FIR and row ops shape-true."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from paper_01_anti_decoy_pnfirtau_amd import ops  # noqa: F401  (registers the fakes)
+
+    B, H, N, D = 2, 3, 100, 64
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        q = torch.empty(B, H, N, D, dtype=torch.bfloat16, device="cuda")
+        tau = torch.empty((), device="cuda")
+        o, o_lo, M, Z, Nm, mask = torch.ops.pnfx.flash_fwd(q, q, q, tau, 0.125, 0.5, True,
+                                                           True, False, True)
+        assert o.shape == o_lo.shape == (B, H, N, D) and o.is_contiguous()
+        assert M.shape == Z.shape == (B, H, N) and M.dtype == Z.dtype == torch.float32
+        assert Nm.shape == (B, H, N) and Nm.dtype == torch.int32
+        assert mask.shape == (B * H, 4, 2) and mask.dtype == torch.uint8
+        ob = torch.ops.pnfx.flash_fwd(q, q, q, tau, 0.125, 0.5, True, True, True, False)
+        assert ob[0].shape == (B, H, N, D) and ob[0].transpose(1, 2).is_contiguous()
+        assert ob[4].numel() == 0  # no tie counts unless asked for
+        dq, dk, dv, dt = torch.ops.pnfx.flash_bwd(q, q, q, tau, o, o_lo, o, M, Z, mask, 0.125,
+                                                  0.5, True, True)
+        assert dq.shape == dk.shape == dv.shape == (B, H, N, D) and dq.is_contiguous()
+        assert dt.shape == (1,) and dt.dtype == torch.float32
+        f = torch.ops.pnfx.flash_fwd_fir(q, q, q, tau, torch.empty(7, device="cuda"), 0.125,
+                                         0.5, True, True)
+        assert [t.shape for t in f] == [(B, H, N, D)] * 2 + [(B, H, N)] * 2 + [(B * H, 4, 2)]
+        x = torch.empty(B, N, 192, dtype=torch.bfloat16, device="cuda")
+        assert torch.ops.pnfx.fir_fwd(x, torch.empty(7, device="cuda")).shape == x.shape
+        raw = torch.empty(B, H, N, N, device="cuda")
+        w, Mr, Zr, Nr = torch.ops.pnfx.pn_rows_fwd(raw, tau, 0.125, 10.0, 0.5, True, True)
+        assert w.shape == raw.shape and Mr.shape == Zr.shape == Nr.shape == (B * H * N,)
+        d_raw, dtr = torch.ops.pnfx.pn_rows_bwd(w, raw, tau, Mr, Zr, Nr, 0.125, 10.0, 0.5, True,
+                                                True)
+        assert d_raw.shape == raw.shape and dtr.shape == (B * H * N,)
+
+
 def test_tile_mask_shape_and_its_length_limit():
     """The forward's silence map is [B*H, ceil(N/32), ceil(N/64)] bytes -- N^2/2048 per (b, h) --
     and is not formed past MASK_MAX_N (the backward then recomputes every tile)."""
