@@ -42,9 +42,11 @@ void* stream_of(const Tensor& t) {
   return c10::hip::getCurrentHIPStream(t.device().index()).stream();
 }
 
-Tensor tau32(const Tensor& tau) {
-  Tensor t = tau.reshape({1});
-  return t.scalar_type() == at::kFloat ? t : t.to(at::kFloat);
+// tau as one fp32 value on the operands' device (the kernels read tau[0] there)
+Tensor tau32(const Tensor& tau, const Tensor& like) {
+  TORCH_CHECK_VALUE(tau.numel() == 1, "tau must hold one value, got shape ", tau.sizes());
+  if (tau.scalar_type() == at::kFloat && tau.device() == like.device()) return tau;
+  return tau.reshape({1}).to(like.device(), at::kFloat);
 }
 
 // -------------------------------------------------------------------------------- FIR
@@ -98,7 +100,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> pn_rows_fwd_cuda(const Tensor& raw, c
     return {w.view(raw.sizes()), M, Z, Nm};
   }
   const c10::DeviceGuard guard(raw.device());
-  const Tensor t32 = tau32(tau);
+  const Tensor t32 = tau32(tau, raw);
   check_rc(pnfx_pn_rows_fwd(r2.data_ptr(), N, w.data_ptr(), N, M.data_ptr<float>(),
                             Z.data_ptr<float>(), Nm.data_ptr<int32_t>(), R, N,
                             t32.data_ptr<float>(), (float)scale, (float)p, (float)gamma,
@@ -119,7 +121,7 @@ std::tuple<Tensor, Tensor> pn_rows_bwd_cuda(const Tensor& dw, const Tensor& raw,
   Tensor dt = at::empty({R}, raw.options().dtype(at::kFloat));
   if (r2.numel() == 0) return {d.view(raw.sizes()), dt.zero_()};
   const c10::DeviceGuard guard(raw.device());
-  const Tensor t32 = tau32(tau);
+  const Tensor t32 = tau32(tau, raw);
   check_rc(pnfx_pn_rows_bwd(g2.data_ptr(), N, r2.data_ptr(), N, M.data_ptr<float>(),
                             Z.data_ptr<float>(), Nmax.data_ptr<int32_t>(), d.data_ptr(), N,
                             dt.data_ptr<float>(), R, N, t32.data_ptr<float>(), (float)scale,
@@ -230,9 +232,10 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> flash_fwd_cuda(
                         q.options().dtype(at::kInt));
   Tensor mask = at::empty({ms[0], ms[1], ms[2]}, q.options().dtype(at::kByte));
   if (rows == 0) return {o, o_lo, M, Z, Nm, mask};  // empty input: empty outputs
-  Tensor ws = at::empty({nws}, q.options().dtype(at::kByte));
+  Tensor ws;
+  if (nws) ws = at::empty({nws}, q.options().dtype(at::kByte));
   const c10::DeviceGuard guard(q.device());
-  const Tensor t32 = tau32(tau);
+  const Tensor t32 = tau32(tau, q);
   check_rc(pnfx_flash_fwd(q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(),
                           k.stride(0), k.stride(1), k.stride(2), v.data_ptr(), v.stride(0),
                           v.stride(1), v.stride(2), o.data_ptr(), o.stride(0), o.stride(1),
@@ -283,7 +286,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> flash_bwd_cuda(
   const c10::DeviceGuard guard(q.device());
   const int64_t wsb = pnfx_flash_bwd_workspace_size(B, H, N, D);
   Tensor ws = at::empty({wsb}, q.options().dtype(at::kByte));
-  const Tensor t32 = tau32(tau);
+  const Tensor t32 = tau32(tau, q);
   check_rc(pnfx_flash_bwd(
                q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0),
                k.stride(1), k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
@@ -315,7 +318,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> flash_fwd_fir_cuda(
   Tensor mask = at::empty({ms[0], ms[1], ms[2]}, q.options().dtype(at::kByte));
   if (B * H * N == 0) return {o, o_lo, M, Z, mask};
   const c10::DeviceGuard guard(q.device());
-  const Tensor t32 = tau32(tau);
+  const Tensor t32 = tau32(tau, q);
   check_rc(pnfx_flash_fwd_fir(q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), kr.data_ptr(),
                               kr.stride(0), kr.stride(1), kr.stride(2), v.data_ptr(), v.stride(0),
                               v.stride(1), v.stride(2), o.data_ptr(), o.stride(0), o.stride(1),
@@ -389,7 +392,7 @@ class RowsFn : public torch::autograd::Function<RowsFn> {
                             ctx->saved_data["causal"].toBool());
     // fp64 sum of the row partials, as src/triton_pnfirtau.py:784
     none[0] = d;
-    none[1] = dt.sum(at::kDouble).to(s[1].scalar_type()).view_as(s[1]);
+    none[1] = dt.sum(at::kDouble).to(s[1].device(), s[1].scalar_type()).view_as(s[1]);
     return none;
   }
 };
@@ -439,7 +442,7 @@ class FlashFn : public torch::autograd::Function<FlashFn> {
     grads[0] = dq;
     grads[1] = dk;
     grads[2] = dv;
-    grads[3] = dt.to(s[3].scalar_type()).view_as(s[3]);
+    grads[3] = dt.to(s[3].device(), s[3].scalar_type()).view_as(s[3]);
     return grads;
   }
 };

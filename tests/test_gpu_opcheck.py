@@ -50,3 +50,21 @@ def test_opcheck_fir_and_row_scores(dev, dtype):
     torch.library.opcheck(torch.ops.pnfx.pn_rows_bwd.default,
                           (torch.randn_like(w), raw.detach(), tau, M, Z, Nm, 0.125, 10.0, 0.5,
                            True, True))
+
+
+def test_tau_on_the_host_is_moved_to_the_device(dev):
+    """The kernels read tau on the device: a CPU (or bf16) tau tensor is brought to the
+    operands' device as fp32 by the op, and its gradient comes back on tau's own device."""
+    B, H, N, D = 1, 2, 70, 64
+    q, k, v, dO = (seeded((B, H, N, D), 330 + i, torch.bfloat16, dev) for i in range(4))
+    outs = []
+    for tau in (torch.tensor(0.05, device=dev), torch.tensor(0.05), torch.tensor(0.05).bfloat16()):
+        t = tau.clone().requires_grad_(True)
+        o = torch.ops.pnfx.flash_fwd(q, k, v, t, 0.125, 0.5, True, True, False, False)[0]
+        o.backward(dO)
+        assert t.grad.device == tau.device and t.grad.dtype == tau.dtype
+        outs.append((o, float(t.grad)))
+    for o, g in outs[1:2]:  # a CPU fp32 tau: exactly the device result
+        assert torch.equal(o, outs[0][0]) and g == outs[0][1]
+    # bf16 tau: 0.05 rounds to bf16, so only closeness
+    assert torch.allclose(outs[2][0].float(), outs[0][0].float(), atol=2e-2, rtol=2e-2)
