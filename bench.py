@@ -483,15 +483,17 @@ def bench_lm(dev, steps=10, warmup=3):
     return out
 
 
-def bench_host_overhead(dev, calls=400):
+def bench_host_overhead(dev, calls=1000):
     """Host time per call of the C++-registered ops (python -> dispatcher -> C ABI -> launch),
     at a shape whose kernels take less GPU time than the host needs to enqueue them: the wall
     time of a loop of calls with no synchronisation inside it (the launches queue up), over
-    the number of calls.  Forward alone (no grad), and a forward + backward through autograd."""
+    the number of calls, best of five loops.  Forward alone (no grad), a forward + backward
+    through autograd, and, for scale on the same host, one torch elementwise add."""
     q, k, v = (torch.randn(1, 1, 64, 64, device=dev).to(torch.bfloat16) for _ in range(3))
     tau = torch.zeros((), device=dev)
     out = {"shape": [1, 1, 64, 64], "dtype": "bf16"}
     flash = torch.ops.pnfx.flash_fwd
+    a = torch.randn(64, 64, device=dev)
 
     def fwd():
         with torch.no_grad():
@@ -505,12 +507,13 @@ def bench_host_overhead(dev, calls=400):
         o = flash(qg, kg, vg, tg, 0.125, 0.5, True, True, False, False)[0]
         torch.autograd.backward(o, dO)
 
-    for name, fn in (("flash_fwd_us_per_call", fwd), ("flash_fwd_bwd_us_per_step", fwd_bwd)):
-        for _ in range(20):
+    for name, fn in (("flash_fwd_us_per_call", fwd), ("flash_fwd_bwd_us_per_step", fwd_bwd),
+                     ("torch_add_us_per_call", lambda: torch.add(a, a))):
+        for _ in range(50):
             fn()
         torch.cuda.synchronize()
         best = float("inf")
-        for _ in range(3):
+        for _ in range(5):
             t0 = time.perf_counter()
             for _ in range(calls):
                 fn()

@@ -341,13 +341,32 @@ c10::OperatorHandle op(const char* name) {
   return c10::Dispatcher::singleton().findSchemaOrThrow(name, "");
 }
 
+// True when autograd has something to record: grad mode on and an input that requires a
+// gradient (or carries a forward-mode tangent, which the Function then refuses as torch
+// does for any custom Function without a jvp).  Otherwise the op runs straight below
+// autograd, with no graph node built: the host time of an inference call.
+bool records(std::initializer_list<const Tensor*> ts) {
+  for (const Tensor* t : ts) {
+    if (t->defined() && t->_fw_grad(/*level=*/0).defined()) return true;
+  }
+  if (!at::GradMode::is_enabled()) return false;
+  for (const Tensor* t : ts) {
+    if (t->defined() && t->requires_grad()) return true;
+  }
+  return false;
+}
+
+const auto& fir_fwd_op() {
+  static auto h = op("pnfx::fir_fwd").typed<Tensor(const Tensor&, const Tensor&)>();
+  return h;
+}
+
 class FirFn : public torch::autograd::Function<FirFn> {
  public:
   static Tensor forward(AutogradContext* ctx, const Tensor& x, const Tensor& taps) {
     at::AutoDispatchBelowADInplaceOrView guard;
-    static auto fwd = op("pnfx::fir_fwd").typed<Tensor(const Tensor&, const Tensor&)>();
     ctx->save_for_backward({taps});
-    return fwd.call(x, taps);
+    return fir_fwd_op().call(x, taps);
   }
   static variable_list backward(AutogradContext* ctx, variable_list gy) {
     static auto bwd = op("pnfx::fir_bwd").typed<Tensor(const Tensor&, const Tensor&)>();
@@ -356,17 +375,27 @@ class FirFn : public torch::autograd::Function<FirFn> {
   }
 };
 
-Tensor fir_fwd_autograd(const Tensor& x, const Tensor& taps) { return FirFn::apply(x, taps); }
+Tensor fir_fwd_autograd(const Tensor& x, const Tensor& taps) {
+  if (!records({&x, &taps})) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    return fir_fwd_op().call(x, taps);
+  }
+  return FirFn::apply(x, taps);
+}
+
+const auto& rows_fwd_op() {
+  static auto h = op("pnfx::pn_rows_fwd")
+                      .typed<std::tuple<Tensor, Tensor, Tensor, Tensor>(
+                          const Tensor&, const Tensor&, double, double, double, bool, bool)>();
+  return h;
+}
 
 class RowsFn : public torch::autograd::Function<RowsFn> {
  public:
   static variable_list forward(AutogradContext* ctx, const Tensor& raw, const Tensor& tau,
                                double scale, double p, double gamma, bool has_gamma, bool causal) {
     at::AutoDispatchBelowADInplaceOrView guard;
-    static auto fwd = op("pnfx::pn_rows_fwd")
-                          .typed<std::tuple<Tensor, Tensor, Tensor, Tensor>(
-                              const Tensor&, const Tensor&, double, double, double, bool, bool)>();
-    auto [w, M, Z, Nm] = fwd.call(raw, tau, scale, p, gamma, has_gamma, causal);
+    auto [w, M, Z, Nm] = rows_fwd_op().call(raw, tau, scale, p, gamma, has_gamma, causal);
     ctx->mark_non_differentiable({M, Z, Nm});
     ctx->set_materialize_grads(false);
     ctx->save_for_backward({raw, tau, M, Z, Nm});
@@ -401,8 +430,20 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> pn_rows_fwd_autograd(const Tensor& ra
                                                                 const Tensor& tau, double scale,
                                                                 double p, double gamma,
                                                                 bool has_gamma, bool causal) {
+  if (!records({&raw, &tau})) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    return rows_fwd_op().call(raw, tau, scale, p, gamma, has_gamma, causal);
+  }
   auto r = RowsFn::apply(raw, tau, scale, p, gamma, has_gamma, causal);
   return {r[0], r[1], r[2], r[3]};
+}
+
+const auto& flash_fwd_op() {
+  static auto h = op("pnfx::flash_fwd")
+                      .typed<std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor>(
+                          const Tensor&, const Tensor&, const Tensor&, const Tensor&, double,
+                          double, bool, bool, bool, bool)>();
+  return h;
 }
 
 class FlashFn : public torch::autograd::Function<FlashFn> {
@@ -411,12 +452,8 @@ class FlashFn : public torch::autograd::Function<FlashFn> {
                                const Tensor& v, const Tensor& tau, double scale, double gamma,
                                bool has_gamma, bool causal, bool o_bnhd, bool with_nmax) {
     at::AutoDispatchBelowADInplaceOrView guard;
-    static auto fwd = op("pnfx::flash_fwd")
-                          .typed<std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor>(
-                              const Tensor&, const Tensor&, const Tensor&, const Tensor&, double,
-                              double, bool, bool, bool, bool)>();
-    auto [o, o_lo, M, Z, Nm, mask] =
-        fwd.call(q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd, with_nmax);
+    auto [o, o_lo, M, Z, Nm, mask] = flash_fwd_op().call(q, k, v, tau, scale, gamma, has_gamma,
+                                                         causal, o_bnhd, with_nmax);
     ctx->mark_non_differentiable({o_lo, M, Z, Nm, mask});
     ctx->set_materialize_grads(false);
     ctx->save_for_backward({q, k, v, tau, o, o_lo, M, Z, mask});
@@ -450,6 +487,10 @@ class FlashFn : public torch::autograd::Function<FlashFn> {
 std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> flash_fwd_autograd(
     const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& tau, double scale,
     double gamma, bool has_gamma, bool causal, bool o_bnhd, bool with_nmax) {
+  if (!records({&q, &k, &v, &tau})) {
+    at::AutoDispatchBelowADInplaceOrView guard;
+    return flash_fwd_op().call(q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd, with_nmax);
+  }
   auto r = FlashFn::apply(q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd, with_nmax);
   return {r[0], r[1], r[2], r[3], r[4], r[5]};
 }

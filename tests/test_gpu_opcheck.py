@@ -68,3 +68,33 @@ def test_tau_on_the_host_is_moved_to_the_device(dev):
         assert torch.equal(o, outs[0][0]) and g == outs[0][1]
     # bf16 tau: 0.05 rounds to bf16, so only closeness
     assert torch.allclose(outs[2][0].float(), outs[0][0].float(), atol=2e-2, rtol=2e-2)
+
+
+def test_inference_call_skips_the_graph_and_matches(dev):
+    """With grad mode off (or no input requiring a gradient) the op runs below autograd
+    without a graph node: outputs carry no grad_fn and equal those of the recorded call."""
+    B, H, N, D = 1, 2, 96, 64
+    q, k, v = (seeded((B, H, N, D), 340 + i, torch.bfloat16, dev) for i in range(3))
+    tau = torch.tensor(0.02, device=dev)
+    qg = q.clone().requires_grad_(True)
+    rec = torch.ops.pnfx.flash_fwd(qg, k, v, tau, 0.125, 0.5, True, True, False, False)
+    assert rec[0].grad_fn is not None
+    with torch.no_grad():
+        inf = torch.ops.pnfx.flash_fwd(qg, k, v, tau, 0.125, 0.5, True, True, False, False)
+    plain = torch.ops.pnfx.flash_fwd(q, k, v, tau, 0.125, 0.5, True, True, False, False)
+    for outs in (inf, plain):
+        assert all(not t.requires_grad and t.grad_fn is None for t in outs)
+        assert all(torch.equal(a, b) for a, b in zip(outs, rec))
+    x = seeded((2, 50, 32), 343, torch.bfloat16, dev)
+    taps = torch.rand(7, device=dev)
+    y_rec = torch.ops.pnfx.fir_fwd(x.clone().requires_grad_(True), taps)
+    with torch.no_grad():
+        y_inf = torch.ops.pnfx.fir_fwd(x, taps)
+    assert y_rec.grad_fn is not None and y_inf.grad_fn is None and torch.equal(y_rec, y_inf)
+    raw = seeded((1, 2, 40, 40), 344, torch.bfloat16, dev)
+    with torch.inference_mode():
+        w_inf = torch.ops.pnfx.pn_rows_fwd(raw, tau, 0.125, 10.0, 0.5, True, True)
+    w_rec = torch.ops.pnfx.pn_rows_fwd(raw.clone().requires_grad_(True), tau, 0.125, 10.0, 0.5,
+                                       True, True)
+    assert w_rec[0].grad_fn is not None and w_inf[0].grad_fn is None
+    assert all(torch.equal(a, b) for a, b in zip(w_inf, w_rec))
