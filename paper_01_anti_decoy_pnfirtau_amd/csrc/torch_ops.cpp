@@ -49,6 +49,20 @@ Tensor tau32(const Tensor& tau, const Tensor& like) {
   return tau.reshape({1}).to(like.device(), at::kFloat);
 }
 
+// A tensor the forward produced and a backward op is handed back (row statistics, tile
+// mask): the kernels index it by row with no size of their own, so it must have the
+// forward's layout: n contiguous elements of type st on the operands' device.
+void check_saved(const Tensor& t, const char* op_name, const char* name, int64_t n,
+                 at::ScalarType st, const Tensor& like) {
+  TORCH_CHECK_TYPE(t.scalar_type() == st, op_name, ": ", name, " is ", t.scalar_type(),
+                   ", the forward's is ", st);
+  TORCH_CHECK_VALUE(t.numel() == n && t.is_contiguous(), op_name, ": ", name,
+                    " must be the forward's contiguous ", n, " elements, got shape ", t.sizes(),
+                    " with strides ", t.strides());
+  TORCH_CHECK_VALUE(t.device() == like.device(), op_name, ": ", name, " is on ", t.device(),
+                    ", the operands on ", like.device());
+}
+
 // -------------------------------------------------------------------------------- FIR
 // x [B,N,C] or [B,H,N,C] with unit channel stride, seen as 4-D.
 Tensor fir_call(const Tensor& x_in, const Tensor& taps, bool adjoint) {
@@ -113,8 +127,13 @@ std::tuple<Tensor, Tensor> pn_rows_bwd_cuda(const Tensor& dw, const Tensor& raw,
                                             const Tensor& M, const Tensor& Z, const Tensor& Nmax,
                                             double scale, double p, double gamma, bool has_gamma,
                                             bool causal) {
+  TORCH_CHECK_VALUE(dw.sizes() == raw.sizes(), "pn_rows_bwd: dw has shape ", dw.sizes(),
+                    ", raw ", raw.sizes());
   const int64_t N = raw.size(-1);
   const int64_t R = n_rows(raw);
+  check_saved(M, "pn_rows_bwd", "M", R, at::kFloat, raw);
+  check_saved(Z, "pn_rows_bwd", "Z", R, at::kFloat, raw);
+  check_saved(Nmax, "pn_rows_bwd", "Nmax", R, at::kInt, raw);
   const Tensor r2 = raw.contiguous().view({R, N});
   const Tensor g2 = dw.to(raw.scalar_type()).contiguous().view({R, N});
   Tensor d = at::empty_like(r2);
@@ -278,6 +297,12 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> flash_bwd_cuda(
   const Tensor dout = bhnd(do_in.scalar_type() == q.scalar_type() ? do_in : do_in.to(q.scalar_type()),
                            "dO", bf);
   const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
+  check_saved(M, "flash_bwd", "M", B * H * N, at::kFloat, q);
+  check_saved(Z, "flash_bwd", "Z", B * H * N, at::kFloat, q);
+  if (mask.numel()) {  // the forward's tile mask, or none (every causal tile recomputed)
+    const auto ms = mask_shape(B, H, N);
+    check_saved(mask, "flash_bwd", "mask", ms[0] * ms[1] * ms[2], at::kByte, q);
+  }
   // dQ, dK, dV and dtau, each its own allocation (returned to autograd as the inputs' grads)
   Tensor dq = at::empty({B, H, N, D}, q.options()), dk = at::empty({B, H, N, D}, q.options());
   Tensor dv = at::empty({B, H, N, D}, q.options());

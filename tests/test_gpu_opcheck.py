@@ -98,3 +98,36 @@ def test_inference_call_skips_the_graph_and_matches(dev):
                                        True, True)
     assert w_rec[0].grad_fn is not None and w_inf[0].grad_fn is None
     assert all(torch.equal(a, b) for a, b in zip(w_inf, w_rec))
+
+
+def test_backward_ops_refuse_statistics_of_another_shape(dev):
+    """The backward ops index the forward's statistics and tile mask by row: tensors of
+    another size, type or layout are refused on the host, before any launch."""
+    B, H, N, D = 1, 2, 96, 64
+    q, k, v, dO = (seeded((B, H, N, D), 350 + i, torch.bfloat16, dev) for i in range(4))
+    tau = torch.tensor(0.0, device=dev)
+    o, o_lo, M, Z, _, mask = torch.ops.pnfx.flash_fwd(q, k, v, tau, 0.125, 0.5, True, True,
+                                                      False, False)
+    bwd = torch.ops.pnfx.flash_bwd
+
+    def call(M_=M, Z_=Z, mask_=mask):
+        return bwd(q, k, v, tau, o, o_lo, dO, M_, Z_, mask_, 0.125, 0.5, True, True)
+
+    ref = call()
+    with pytest.raises(ValueError, match="M must be"):
+        call(M_=M[..., :-1].contiguous())
+    with pytest.raises(TypeError, match="Z is"):
+        call(Z_=Z.double())
+    with pytest.raises(ValueError, match="M must be"):
+        call(M_=M.transpose(1, 2).contiguous().transpose(1, 2))  # right size, not contiguous
+    with pytest.raises(ValueError, match="mask must be"):
+        call(mask_=mask[:, :-1].contiguous())
+    # no mask at all is allowed (every causal tile recomputed), with the same results
+    assert all(torch.equal(a, b) for a, b in zip(call(mask_=mask[:0]), ref))
+    raw = seeded((1, 2, 40, 40), 355, torch.bfloat16, dev)
+    w, Mr, Zr, Nm = torch.ops.pnfx.pn_rows_fwd(raw, tau, 0.125, 10.0, 0.5, True, True)
+    rbwd = torch.ops.pnfx.pn_rows_bwd
+    with pytest.raises(TypeError, match="Nmax is"):
+        rbwd(torch.ones_like(w), raw, tau, Mr, Zr, Nm.float(), 0.125, 10.0, 0.5, True, True)
+    with pytest.raises(ValueError, match="dw has shape"):
+        rbwd(torch.ones_like(w)[..., :-1], raw, tau, Mr, Zr, Nm, 0.125, 10.0, 0.5, True, True)
