@@ -778,3 +778,32 @@ def _check_random_case(dev, case):
     (1, 2, 428, 128, 0.0, None, False, 128 ** -0.5, 1.0, False, torch.bfloat16)])
 def test_flash_d128_peaked_rows_match_oracle(dev, case):
     _check_random_case(dev, case)
+
+
+# Draws of a 3840-draw sweep (32 more seeds, run once, not part of the suite) that go past the
+# bar, each reproduced to its printed digits by a CPU emulation of the kernels' rounding
+# points (float64 elsewhere), so none is a kernel fault:
+# * dQ (two draws): D = <dO, O>/g comes from O weighted by bf16-rounded P, as the reference's
+#   does, and in these rows the dS k terms nearly cancel, so the 2^-9 relative shift of D
+#   crosses a bf16 rounding boundary of dS; emulated ratios 1.34 and 1.89 against bars of
+#   1.19 (reference rounding 0.95) and 1.90 (1.52).
+# * dK (one draw): one element at 1.04 of a bar of 1 (emulated 1.04; the reference rounding's
+#   ratio on that tensor is 0.80).
+# * dtau (one draw, N = 4): dtau is summed from the bf16-rounded dS the dQ product consumes,
+#   where the reference sums the unrounded du; with four keys whose roundings go the same
+#   way the sum moves by 0.19 against a bar of 0.188 (2e-3 of |dtau| + sum |du| = 94.2).
+#   Emulated: the rounded sum gives 2.9063, the unrounded 2.7129, the oracle 2.7124.
+KNOWN_EXCURSIONS = [
+    (1, 1, 187, 64, 0.0, None, True, 0.173, 0.5, True, torch.bfloat16),
+    (2, 2, 579, 16, 0.0, 0.5, False, 0.25, 1.0, True, torch.bfloat16),
+    (2, 1, 699, 16, -0.149, None, False, 0.25, 1.0, False, torch.bfloat16),
+    (2, 3, 4, 128, 0.306, None, True, 0.082, 2.0, False, torch.bfloat16),
+]
+
+
+@pytest.mark.xfail(reason="bf16 rounding tails of dS (and, for dtau, its sum over rounded dS) "
+                          "reproduced by a CPU emulation of the kernels' rounding points",
+                   strict=False)
+@pytest.mark.parametrize("case", KNOWN_EXCURSIONS)
+def test_flash_known_excursions_wider_sweep(dev, case):
+    _check_random_case(dev, case)
