@@ -131,3 +131,30 @@ def test_backward_ops_refuse_statistics_of_another_shape(dev):
         rbwd(torch.ones_like(w), raw, tau, Mr, Zr, Nm.float(), 0.125, 10.0, 0.5, True, True)
     with pytest.raises(ValueError, match="dw has shape"):
         rbwd(torch.ones_like(w)[..., :-1], raw, tau, Mr, Zr, Nm, 0.125, 10.0, 0.5, True, True)
+
+
+@pytest.mark.parametrize("training", [True, False])
+def test_module_compiles_without_graph_breaks(dev, training):
+    """PnFirTauFlashMHA under torch.compile (AOTAutograd, no code generation) traces the pnfx
+    ops into one graph, and the compiled forward (and backward) give the eager results."""
+    from paper_01_anti_decoy_pnfirtau_amd import PnFirConfig, PnFirTauFlashMHA
+    torch.manual_seed(7)
+    m = PnFirTauFlashMHA(PnFirConfig(d_model=64, n_heads=4)).to(dev).bfloat16()
+    with torch.no_grad():
+        m.score_tau.fill_(0.05)
+    x = seeded((2, 96, 64), 360, torch.bfloat16, dev)
+    torch._dynamo.reset()
+    cm = torch.compile(m, backend="aot_eager", fullgraph=True, dynamic=False)
+    if training:
+        outs = []
+        for f in (m, cm):
+            xg = x.clone().requires_grad_(True)
+            m.zero_grad(set_to_none=True)
+            y = f(xg)
+            y.float().square().sum().backward()
+            outs.append((y, xg.grad, m.qkv.weight.grad, m.score_tau.grad))
+        for a, b in zip(*outs):
+            assert torch.equal(a, b)
+    else:
+        with torch.no_grad():
+            assert torch.equal(m(x), cm(x))
