@@ -526,11 +526,10 @@ def bench_host_overhead(dev, calls=1000):
 MHA6 = dict(n_layers=6, d_model=64, n_heads=4, N=1024, B=16)
 
 
-def bench_mha6(dev, steps=60, warmup=10):
-    """The reference's graph experiment (experiments/exp4c_cuda_graphs.py:75-108): a residual
-    stack of 6 PnFirTauFlashMHA layers (d_model 64, 4 heads, N 1024, B 16, bf16 autocast),
-    one forward+backward per step, eager and replayed from one HIP graph, at tau = -0.5 (all
-    tiles active) and +2.5 (all tiles silent)."""
+def _mha6_stack(dev):
+    """The reference's graph experiment's stack (experiments/exp4c_cuda_graphs.py:75-108): 6
+    residual PnFirTauFlashMHA layers (d_model 64, 4 heads, N 1024, B 16, bf16 autocast) and
+    its step, one forward+backward.  Returns (layers, step)."""
     from paper_01_anti_decoy_pnfirtau_amd import PnFirConfig, PnFirTauFlashMHA
 
     torch.manual_seed(42)
@@ -552,6 +551,50 @@ def bench_mha6(dev, steps=60, warmup=10):
                 h = h + lyr(h)
         h.backward(dy)
 
+    return layers, step
+
+
+def bench_mha6_host(dev, steps=20, warmup=20):
+    """Where the eager mha6 step's host time goes: torch's profiler (CPU side) over `steps`
+    eager steps at tau = -0.5, self CPU time per step by operator, and the shares of torch's
+    GEMM dispatch (aten::mm) and of the pnfx ops with their autograd nodes."""
+    from torch.profiler import ProfilerActivity, profile
+
+    layers, step = _mha6_stack(dev)
+    with torch.no_grad():
+        for lyr in layers:
+            lyr.score_tau.fill_(-0.5)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CPU]) as prof:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    ka = prof.key_averages()
+    print(ka.table(sort_by="self_cpu_time_total", row_limit=25, max_name_column_width=60),
+          file=sys.stderr)
+    per_step = lambda us: round(us / steps, 1)  # noqa: E731
+    total = sum(e.self_cpu_time_total for e in ka)
+    mm = sum(e.self_cpu_time_total for e in ka if e.key == "aten::mm")
+    pnfx = sum(e.self_cpu_time_total for e in ka if "pnfx::" in e.key or "FlashFn" in e.key
+               or "FirFn" in e.key)
+    return {"mha6_host_profile": {
+        "what": "torch.profiler CPU self time per eager mha6 step (tau=-0.5), profiler overhead included",
+        "steps": steps, "self_cpu_us_per_step": per_step(total),
+        "aten_mm_us_per_step": per_step(mm),
+        "aten_mm_calls_per_step": sum(e.count for e in ka if e.key == "aten::mm") // steps,
+        "pnfx_ops_and_nodes_us_per_step": per_step(pnfx),
+        "top": [{"op": e.key, "self_us_per_step": per_step(e.self_cpu_time_total),
+                 "calls_per_step": e.count // steps}
+                for e in sorted(ka, key=lambda e: -e.self_cpu_time_total)[:12]]}}
+
+
+def bench_mha6(dev, steps=60, warmup=10):
+    """The reference's graph experiment (experiments/exp4c_cuda_graphs.py:75-108): the stack of
+    _mha6_stack, one forward+backward per step, eager and replayed from one HIP graph, at
+    tau = -0.5 (all tiles active) and +2.5 (all tiles silent)."""
+    layers, step = _mha6_stack(dev)
     out = {"config": MHA6}
     for tau in (-0.5, 2.5):
         with torch.no_grad():
@@ -720,7 +763,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", choices=["flash", "flash_c5", "flash_silent", "fir", "fir_sweep", "fir_fused", "copy", "host", "f32",
-                                       "lm", "mha6", "ref", "kernels", "rows"],
+                                       "lm", "mha6", "mha6_host", "ref", "kernels", "rows"],
                     default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -755,6 +798,9 @@ def main():
         return
     if args.only == "mha6":
         print(json.dumps(bench_mha6(dev)))
+        return
+    if args.only == "mha6_host":
+        print(json.dumps(bench_mha6_host(dev)))
         return
     if args.only == "ref":
         print(json.dumps(bench_reference_configs(dev)))
