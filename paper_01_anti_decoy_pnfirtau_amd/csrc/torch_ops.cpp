@@ -268,6 +268,18 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> flash_fwd_cuda(
   return {o, o_lo, M, Z, Nm, mask};
 }
 
+// A [B,H,N,D] gradient laid out in its input's dimension order: for an input whose head
+// stride is below its row stride (the heads of one [B,N,H*D] row, as the modules split a qkv
+// projection) a [B,H,N,D] view of [B,N,H,D] memory, so that autograd's merge of the heads back
+// into rows is a view and not a copy; [B,H,N,D] rows otherwise.  The fake kernel (ops.py)
+// follows the same rule.
+Tensor grad_like(const Tensor& t) {
+  const int64_t B = t.size(0), H = t.size(1), N = t.size(2), D = t.size(3);
+  if (H > 1 && N > 1 && t.stride(1) < t.stride(2))
+    return at::empty({B, N, H, D}, t.options()).permute({0, 2, 1, 3});
+  return at::empty({B, H, N, D}, t.options());
+}
+
 std::tuple<Tensor, Tensor, Tensor, Tensor> flash_bwd_cuda(
     const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, const Tensor& tau,
     const Tensor& o_in, const Tensor& o_lo, const Tensor& do_in, const Tensor& M, const Tensor& Z,
@@ -298,14 +310,14 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> flash_bwd_cuda(
                            "dO", bf);
   const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
   check_saved(M, "flash_bwd", "M", B * H * N, at::kFloat, q);
+  // Each gradient in its input's dimension order (see grad_like).
   check_saved(Z, "flash_bwd", "Z", B * H * N, at::kFloat, q);
   if (mask.numel()) {  // the forward's tile mask, or none (every causal tile recomputed)
     const auto ms = mask_shape(B, H, N);
     check_saved(mask, "flash_bwd", "mask", ms[0] * ms[1] * ms[2], at::kByte, q);
   }
   // dQ, dK, dV and dtau, each its own allocation (returned to autograd as the inputs' grads)
-  Tensor dq = at::empty({B, H, N, D}, q.options()), dk = at::empty({B, H, N, D}, q.options());
-  Tensor dv = at::empty({B, H, N, D}, q.options());
+  Tensor dq = grad_like(q_in), dk = grad_like(k_in), dv = grad_like(v_in);
   Tensor dtau = at::empty({1}, q.options().dtype(at::kFloat));
   if (B * H * N == 0) return {dq, dk, dv, dtau.zero_()};  // -(sum over no scores) = 0
   const c10::DeviceGuard guard(q.device());

@@ -133,12 +133,21 @@ def _(q, k, v, tau, scale, gamma, has_gamma, causal, o_bnhd, with_nmax):
     return o, o_lo, f(torch.float32), f(torch.float32), nm, mask
 
 
+def _grad_like(t: Tensor) -> Tensor:
+    """The backward op's gradient layout (csrc/torch_ops.cpp, grad_like): a [B,H,N,D] view of
+    [B,N,H,D] memory when the input's head stride is below its row stride, else [B,H,N,D]."""
+    B, H, N, D = t.shape
+    if H > 1 and N > 1 and t.stride(1) < t.stride(2):
+        return t.new_empty((B, N, H, D)).permute(0, 2, 1, 3)
+    return t.new_empty((B, H, N, D))
+
+
 @torch.library.register_fake("pnfx::flash_bwd")
 def _(q, k, v, tau, o, o_lo, do, M, Z, mask, scale, gamma, has_gamma, causal):
-    return (torch.empty_like(q, memory_format=torch.contiguous_format),
-            torch.empty_like(k, memory_format=torch.contiguous_format),
-            torch.empty_like(v, memory_format=torch.contiguous_format),
-            q.new_empty(1, dtype=torch.float32))
+    if q.shape[-1] not in (16, 32, 64, 128):  # padded head sizes: contiguous slices
+        return (q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape),
+                q.new_empty(1, dtype=torch.float32))
+    return _grad_like(q), _grad_like(k), _grad_like(v), q.new_empty(1, dtype=torch.float32)
 
 
 @torch.library.register_fake("pnfx::flash_fwd_fir")

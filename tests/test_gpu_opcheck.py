@@ -158,3 +158,25 @@ def test_module_compiles_without_graph_breaks(dev, training):
     else:
         with torch.no_grad():
             assert torch.equal(m(x), cm(x))
+
+
+def test_backward_gradients_follow_the_inputs_dimension_order(dev):
+    """For q/k/v that are head views of [B,N,H*D] rows (as the modules split a qkv projection)
+    the gradients come back as views of [B,N,H,D] memory, so that merging their heads is free;
+    values are those of the contiguous call, and opcheck holds the fake kernel to the layout."""
+    B, H, N, D = 2, 4, 80, 32
+    qkv = seeded((B, N, 3, H, D), 370, torch.bfloat16, dev)
+    q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+    dO = seeded((B, H, N, D), 374, torch.bfloat16, dev)
+    tau = torch.tensor(0.01, device=dev)
+    fwd = torch.ops.pnfx.flash_fwd(q, k, v, tau, D ** -0.5, 0.5, True, True, False, False)
+    o, o_lo, M, Z, _, mask = fwd
+    args = (o, o_lo, dO, M, Z, mask, D ** -0.5, 0.5, True, True)
+    grads = torch.ops.pnfx.flash_bwd(q, k, v, tau, *args)
+    qc, kc, vc = (t.contiguous() for t in (q, k, v))
+    ref = torch.ops.pnfx.flash_bwd(qc, kc, vc, tau, *args)
+    for g, r in zip(grads[:3], ref[:3]):
+        assert g.transpose(1, 2).is_contiguous() and r.is_contiguous()
+        assert torch.equal(g, r)
+    assert torch.equal(grads[3], ref[3])
+    torch.library.opcheck(torch.ops.pnfx.flash_bwd.default, (q, k, v, tau, *args))
