@@ -301,3 +301,17 @@ def test_fir_entry_point_takes_eager_path_on_cpu(K):
         assert torch.equal(triton_causal_fir(_t(f["x"]), taps), _t(f["y_f32"]))
         assert torch.equal(triton_causal_fir(_t(f["x_bf16"]), taps).view(torch.int16),
                            _t(f["y_bf16"]).view(torch.int16))
+
+
+def test_missing_libraries_fail_loudly(monkeypatch):
+    """The product path has no fallback: without libpnfx.so (the C ABI) or _pnfx_torch.so (the
+    operator registration) loading raises PnfxError instead of running anything else."""
+    from paper_01_anti_decoy_pnfirtau_amd import _lib, ops
+    monkeypatch.setattr(_lib, "LIB_PATH", "/nonexistent/libpnfx.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(_lib.PnfxError, match="not built"):
+        _lib.lib()
+    monkeypatch.undo()
+    monkeypatch.setattr(ops, "TORCH_OPS_PATH", "/nonexistent/_pnfx_torch.so")
+    with pytest.raises(_lib.PnfxError, match="not built"):
+        ops._load()
