@@ -807,3 +807,32 @@ KNOWN_EXCURSIONS = [
 @pytest.mark.parametrize("case", KNOWN_EXCURSIONS)
 def test_flash_known_excursions_wider_sweep(dev, case):
     _check_random_case(dev, case)
+
+
+@pytest.mark.parametrize("B, H, N, D", [(64, 32, 96, 32), (31, 33, 200, 64)])
+def test_flash_many_slices_match_oracle_per_slice(dev, B, H, N, D):
+    """Grids of thousands of workgroups: 2048 (b, h) slices, and 1023 slices of two query
+    blocks (a block count that is not a multiple of the eight XCDs the dispatch order
+    stripes over).  Slices are independent, so a spread of them is checked against the
+    oracle one slice at a time; dtau, a sum over every slice, against the oracle's sum."""
+    scale, tau, gamma = D ** -0.5, 0.05, 0.5
+    q, k, v, dO = (seeded((B, H, N, D), 380 + i, torch.bfloat16, dev) for i in range(4))
+    o, dq, dk, dv, dt = _run(q, k, v, tau, dO, scale, gamma, True)
+    picks = sorted({(0, 0), (B - 1, H - 1), (B // 2, H // 3), (B // 3, H - 1), (1, 5 % H),
+                    (B - 2, 0)})
+    for b, h in picks:
+        def sl(t):
+            return t[b:b + 1, h:h + 1]
+        Of, _, _, _, rdq, rdk, rdv, _, _ = flash_oracle(sl(q), sl(k), sl(v), tau, sl(dO), scale,
+                                                        gamma, True)
+        em = flash_reference_rounding(sl(q), sl(k), sl(v), tau, sl(dO), scale, gamma, True)
+        for name, got, want in (("O", sl(o), Of), ("dq", sl(dq), rdq), ("dk", sl(dk), rdk),
+                                ("dv", sl(dv), rdv)):
+            assert_bf16_close(to_np64(got), want, name, em.get(name))
+    rdt, dabs = 0.0, 0.0
+    for b0 in range(0, B, 8):  # the oracle's dtau over every slice, eight batches at a time
+        parts = [to_np64(t[b0:b0 + 8]) for t in (q, k, v, dO)]
+        _, _, _, t_, a_ = O.flash_bwd(parts[0], parts[1], parts[2], tau, parts[3], scale, gamma,
+                                      True, return_abs=True)
+        rdt, dabs = rdt + t_, dabs + a_
+    assert_sum_close(float(dt), rdt, dabs, BF16_ATOL, "dtau")
