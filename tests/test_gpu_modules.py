@@ -97,14 +97,14 @@ def test_reference_fp32_parity_protocol(dev):
         x1 = x.clone().requires_grad_(True)
         y1 = m_ref(x1)
         y1.backward(dy)
-        out_n, dx_n = float(y1.abs().max()), float(x1.grad.abs().max())
+        out_n, dx_n = float(y1.detach().abs().max()), float(x1.grad.abs().max())
         dtau_n = float(m_ref.score_tau.grad.abs())
         for name, m in mods.items():
             x2 = x.clone().requires_grad_(True)
             y2 = m(x2)
             y2.backward(dy)
             torch.cuda.synchronize()
-            od = float((y1 - y2).abs().max())
+            od = float((y1 - y2).detach().abs().max())
             dd = float((x1.grad - x2.grad).abs().max())
             td = float((m_ref.score_tau.grad - m.score_tau.grad).abs())
             PARITY_LOG.append({"test": "reference_fp32_parity_protocol", "what": name,

@@ -57,3 +57,19 @@ def test_rows_stats_and_silent_rows(dev):
     np.testing.assert_allclose(Z.cpu().numpy(), Zo.reshape(-1), rtol=1e-5)
     # row sums equal gate * mass / (mass + 1e-12), i.e. the gate unless the mass is tiny
     np.testing.assert_allclose(w.sum(-1).cpu().numpy().reshape(-1), Wo.sum(-1).reshape(-1), rtol=1e-5, atol=1e-7)
+
+
+def test_rows_of_length_one_and_many_rows(dev):
+    """Score rows of one key (the row's only score is its peak) and a tall stack of short rows."""
+    for shape in ((3, 5, 1, 1), (20000, 3, 3)):
+        raw = torch.randn(shape, device=dev).to(torch.bfloat16)
+        print(f"[rows {tuple(raw.shape)}]", flush=True)
+        tau = torch.tensor(0.1, device=dev)
+        w, M, Z, Nm = torch.ops.pnfx.pn_rows_fwd(raw, tau, 0.5, 10.0, 0.5, True, False)
+        s = raw.float() * 0.5 - 0.1
+        u = s.clamp_min(0)
+        P = (u ** 10)
+        m = u.amax(-1, keepdim=True)
+        g = torch.where(m > 0, m / (m + 0.5), torch.zeros_like(m))
+        ref = P / (P.sum(-1, keepdim=True) + 1e-12) * g
+        torch.testing.assert_close(w.float(), ref, rtol=2e-2, atol=2e-3)
