@@ -144,7 +144,8 @@ def _grads(model, x, amp):
     loss = lm_loss(model, x, amp)
     loss.backward()
     torch.cuda.synchronize()
-    return float(loss), {n: p.grad.detach().double().clone() for n, p in model.named_parameters()}
+    return float(loss.detach()), {n: p.grad.detach().double().clone()
+                                  for n, p in model.named_parameters()}
 
 
 def _rel(a, b):
