@@ -166,3 +166,43 @@ def test_module_inference_takes_the_fused_route_bitwise(dev, monkeypatch):
     with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.bfloat16):
         m(long_x)
     assert len(calls) == 1
+
+
+def _random_fused_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        D = int(rng.choice([16, 32, 64]))
+        per_head = bool(rng.random() < 0.5)
+        # shared taps are the reference's Gaussian ones, defined for odd lengths only
+        K = int(rng.integers(1, 8)) if per_head else int(rng.choice([1, 3, 5, 7]))
+        out.append((int(rng.integers(1, 3)), int(rng.integers(1, 4)), int(rng.integers(1, 700)), D,
+                    float(np.round(rng.uniform(-0.3, 0.4), 3)), bool(rng.random() < 0.75),
+                    K, per_head,
+                    float(rng.choice([D ** -0.5, np.round(rng.uniform(0.05, 0.35), 4)]))))
+    return out
+
+
+@pytest.mark.parametrize("seed", [5, 6, 7, 8])
+def test_fused_fir_forward_random_sweep(dev, seed):
+    """Seeded random shapes (d 16/32/64, N 1..699, K 1..7, shared or per-head taps, tau of
+    either sign, causal or not, power-of-two or arbitrary scale), each against the oracle and
+    bitwise against the two launches it replaces."""
+    for case in _random_fused_cases(30, seed):
+        B, H, N, D, tau, causal, K, per_head, scale = case
+        print(f"[fused fir random {case}]", flush=True)
+        q, kraw, v, taps = _inputs(dev, B, H, N, D, K, per_head)
+        t32 = torch.tensor(tau, device=dev)
+        fo, flo, fM, fZ, fmask = ops.flash_fwd_fused_fir(q, kraw, v, t32, taps, scale, 0.5, True,
+                                                         causal)
+        k = torch.ops.pnfx.fir_fwd(kraw, taps)
+        o, o_lo, M, Z, _, mask = torch.ops.pnfx.flash_fwd(q, k, v, t32, scale, 0.5, True, causal,
+                                                           False, False)
+        torch.cuda.synchronize()
+        for name, a, b in (("O", fo, o), ("O_lo", flo, o_lo), ("M", fM, M), ("Z", fZ, Z),
+                           ("mask", fmask, mask)):
+            assert torch.equal(a.view(torch.uint8) if a.dtype == torch.bfloat16 else a,
+                               b.view(torch.uint8) if b.dtype == torch.bfloat16 else b), name
+        slices = [(b, h) for b in range(B) for h in range(H)]
+        _check_against_oracle(fo, fM, fZ, fmask, q, _fir_oracle(kraw, taps), v, tau, scale,
+                              causal, slices, "fused random")
