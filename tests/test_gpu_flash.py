@@ -505,12 +505,15 @@ def test_flash_silent_tile_bound_off_past_its_tile_limit(dev):
         assert torch.equal(x, y), name
 
 
-def test_flash_backward_is_deterministic(dev):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_flash_backward_is_deterministic(dev, dtype):
+    """No atomics and fixed summation orders (the fp32 kernels' split tiles included): two
+    runs give the same bits."""
     B, H, N, D = 2, 2, 512, 64
-    q = seeded((B, H, N, D), 50, torch.bfloat16, dev)
-    k = seeded((B, H, N, D), 51, torch.bfloat16, dev)
-    v = seeded((B, H, N, D), 52, torch.bfloat16, dev)
-    dO = seeded((B, H, N, D), 53, torch.bfloat16, dev)
+    q = seeded((B, H, N, D), 50, dtype, dev)
+    k = seeded((B, H, N, D), 51, dtype, dev)
+    v = seeded((B, H, N, D), 52, dtype, dev)
+    dO = seeded((B, H, N, D), 53, dtype, dev)
     r1 = _run(q, k, v, 0.0, dO, 1 / 8, 0.5, True)
     r2 = _run(q, k, v, 0.0, dO, 1 / 8, 0.5, True)
     for a, b in zip(r1, r2):
