@@ -839,3 +839,38 @@ def test_flash_many_slices_match_oracle_per_slice(dev, B, H, N, D):
                                       True, return_abs=True)
         rdt, dabs = rdt + t_, dabs + a_
     assert_sum_close(float(dt), rdt, dabs, BF16_ATOL, "dtau")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_flash_past_the_mask_limit_rows_match_oracle(dev, dtype):
+    """N = 65600, past the tile mask's 65536-row limit: the forward records no mask (and, in
+    bf16, runs without its tile list) and the backward recomputes every causal tile.  Rows of
+    O, M and dQ and the last keys' dK and dV against the float64 oracle, as above."""
+    print(f"[flash N=65600 rows {dtype}]", flush=True)
+    B, H, N, D, tau = 1, 1, 65600, 64, 0.05
+    g = torch.Generator().manual_seed(19)
+    q, k, v, dO = [torch.randn(B, H, N, D, generator=g).to(dtype).to(dev) for _ in range(4)]
+    o, dq, dk, dv, _ = _run(q, k, v, tau, dO, None, 0.5, True)
+    _, M, Z, _, mask = flash_pn_fir_tau_attention_with_stats(q, k, v, torch.tensor(tau, device=dev))
+    assert mask.numel() == 0
+    qn, kn, vn, dn = (to_np64(t[0, 0]) for t in (q, k, v, dO))
+    scale = 1.0 / np.sqrt(D)
+    rows = [0, 5, 4096, 65535, 65536] + list(range(N - 4, N))
+    Of, Mo, rq = [], [], []
+    rk, rv = np.zeros((4, D)), np.zeros((4, D))
+    for i in rows:
+        oi, mi, _, _ = O.flash_fwd(qn[i:i + 1], kn[:i + 1], vn[:i + 1], tau, scale, 0.5, False)
+        dqi, dki, dvi, _ = O.flash_bwd(qn[i:i + 1], kn[:i + 1], vn[:i + 1], tau, dn[i:i + 1],
+                                       scale, 0.5, False)
+        Of.append(oi[0]), Mo.append(mi[0]), rq.append(dqi[0])
+        if i >= N - 4:  # row i reaches keys N - 4 .. i
+            rk[:i + 1 - (N - 4)] += dki[N - 4:]
+            rv[:i + 1 - (N - 4)] += dvi[N - 4:]
+    pick = lambda t: to_np64(t[0, 0])[rows]  # noqa: E731
+    check = (assert_bf16_close if dtype == torch.bfloat16
+             else lambda a, b, what: assert_close(a, b, F32_TOL, F32_TOL, what))
+    check(pick(o), np.array(Of), "N=65600 O rows")
+    assert_close(pick(M), np.array(Mo), 1e-5, 1e-5, "N=65600 M rows")
+    check(pick(dq), np.array(rq), "N=65600 dQ rows")
+    check(to_np64(dk[0, 0])[N - 4:], rk, "N=65600 dK last keys")
+    check(to_np64(dv[0, 0])[N - 4:], rv, "N=65600 dV last keys")
